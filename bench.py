@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""Benchmark of the vocabulary-parallel cross entropy on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--workload c2|c3|c1] [--gpus 1]
+
+A step is one forward + backward of the loss over one batch of synthetic
+logits already resident in HBM, through the drop-in
+``nmce.vocab_parallel_cross_entropy`` exactly as nano-megatron's GPT.forward
+calls it (model.py:277-281): target validation, per-shard statistics, the
+cross-shard combine, ``loss.mean()``, ``loss.backward()`` with the gradient
+written in place into the (non-leaf) logits.
+
+Workloads:
+  c2 (default)  TP=1, bf16 logits [8,2048,50304] ~ N(0,1), targets U[0,V)
+  c3            one TP=2 rank's shard: bf16 [4,4096,64128] at vocab offset
+                64128 ~ N(0,1.5^2), targets U[0,128256) (about half not owned);
+                the peer rank's statistics are computed once up front and
+                handed over by an emulated all-gather, the combine is local
+  c1            fp32 [4,256,32000] ~ N(0,2^2) (the reference's CPU config)
+
+Prints one JSON line. ``roofline`` covers the dominant kernel: its
+algorithmic HBM bytes per launch (tokens x vocab x bytes read and written,
+plus per-token statistics) over its average launch time, measured with HIP
+events on the launch stream during the timed steps. ``cpu_baseline`` is the
+torch-CPU restatement of the reference's op sequence (oracle/ce_restate.py)
+timed on this host on a bounded sample of the same workload.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import pathlib
+import platform
+import statistics
+import sys
+import time
+
+ROOT = pathlib.Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "nano-megatron_amd"))
+
+METRIC = "vocab-CE fwd+bwd tokens/s at 1 GPU; % HBM roofline (unfused) / % MFMA peak (fused)"
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+
+WORKLOADS = {
+    "c2": dict(desc="unfused TP=1, bf16 logits [8,2048,50304] ~ N(0,1), targets U[0,50304)",
+               b=8, s=2048, v=50304, tp=1, rank=0, sigma=1.0, dtype="bf16"),
+    "c3": dict(desc="one TP=2 rank's shard, bf16 logits [4,4096,64128] at vocab offset 64128 "
+                    "~ N(0,1.5^2), targets U[0,128256), local combine",
+               b=4, s=4096, v=64128, tp=2, rank=1, sigma=1.5, dtype="bf16"),
+    "c1": dict(desc="fp32 logits [4,256,32000] ~ N(0,2^2), targets U[0,32000), TP=1",
+               b=4, s=256, v=32000, tp=1, rank=0, sigma=2.0, dtype="f32"),
+}
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=100)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="c2")
+    p.add_argument("--no-cpu-baseline", action="store_true",
+                   help="skip the CPU baseline (e.g. under a profiler)")
+    p.add_argument("--cpu-rows", type=int, default=1024,
+                   help="tokens in the CPU baseline sample (full vocabulary width)")
+    return p.parse_args()
+
+
+def host_cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(wl: dict, rows: int) -> dict:
+    """Time the torch-CPU restatement of cross_entropy.py on ``rows`` tokens
+    at the workload's full vocabulary width: 1 warmup, median of 5."""
+    import torch
+    from oracle import ce_restate as R
+
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    v, tp, rank = wl["v"], wl["tp"], wl["rank"]
+    dt = torch.bfloat16 if wl["dtype"] == "bf16" else torch.float32
+    x = (torch.randn(rows, v, generator=g) * wl["sigma"]).to(dt)
+    t = torch.randint(0, v * tp, (rows,), generator=g)
+    start, end = rank * v, (rank + 1) * v
+    hook_args = None
+    if tp > 1:  # peer shard partials, computed before timing (the other rank's work)
+        peer = (torch.randn(rows, v, generator=g) * wl["sigma"]).to(dt)
+        pmax = peer.float().max(-1)[0]
+        gmax = torch.maximum(pmax, x.float().max(-1)[0])
+        pick, psum = R.peer_partials(peer, t, 0, v, gmax)
+        hook_args = (pmax, pick, psum)
+        del peer
+    go = torch.full((rows,), 1.0 / rows)
+
+    def step():
+        hook = R.fixed_peer_all_reduce(*hook_args) if hook_args else None
+        # the reference validates targets first (cross_entropy.py:80-81)
+        if torch.any(t < 0) or torch.any(t >= v * tp):
+            raise ValueError("bad target")
+        loss, saved = R.forward(x, t, start, end, all_reduce=hook)
+        loss.mean()
+        return R.backward(saved, go)
+
+    step()
+    times = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": rows / med,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{rows} tokens x full vocab {v} ({wl['dtype']} logits), torch-CPU restatement "
+                  f"of cross_entropy.py fwd+bwd, median of 5 after 1 warmup; "
+                  f"host {host_cpu_model()}, torch {torch.__version__}",
+        "ms_per_step": med * 1e3,
+    }
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; --gpus must be 1 "
+                          "(the TP exchange is one all-gather of [3, tokens] statistics, "
+                          "not exercised here)"}))
+        return 2
+
+    import torch
+    import nmce
+    import nmce.cross_entropy as ce_mod
+
+    wl = WORKLOADS[args.workload]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    n = wl["b"] * wl["s"]
+    v, tp, rank = wl["v"], wl["tp"], wl["rank"]
+    dt = torch.bfloat16 if wl["dtype"] == "bf16" else torch.float32
+    esize = 2 if dt == torch.bfloat16 else 4
+    start, end = rank * v, (rank + 1) * v
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+    base = (torch.randn(n, v, device=dev, generator=gen) * wl["sigma"]).to(dt)
+    target = torch.randint(0, v * tp, (wl["b"], wl["s"]), device=dev, generator=gen)
+    ctx = nmce.ParallelContext(rank=rank, world_size=tp, tp_size=tp, tp_rank=rank, pp_size=1,
+                               pp_rank=0, dp_size=1, dp_rank=0)
+    if tp > 1:
+        # The other rank's shard: its statistics are what the all-gather would
+        # deliver. Computed once here, handed over by an emulated exchange.
+        peer = (torch.randn(n, v, device=dev, generator=gen) * wl["sigma"]).to(dt)
+        from nmce import _lib as L
+        lib = L.load()
+        peer_stats = torch.empty((3, n), dtype=torch.float32, device=dev)
+        tflat = target.reshape(-1)
+        L.check(lib.nmce_ce_fwd_stats(peer.data_ptr(), L.dtype_code(dt), n, v, v, tflat.data_ptr(),
+                                      0, peer_stats[0].data_ptr(), peer_stats[1].data_ptr(),
+                                      peer_stats[2].data_ptr(), L.stream_handle(dev)), "peer")
+        del peer
+
+        def emulated_all_gather(local, group, world_size):
+            return torch.stack([peer_stats, local])
+
+        ce_mod._exchange_stats = emulated_all_gather
+
+    # Non-leaf logits on the same storage (a view of a leaf), as the LM-head
+    # output is at model.py:277: the gradient goes in place.
+    base.requires_grad_(True)
+    logits = base.view(wl["b"], wl["s"], v)
+
+    def step():
+        base.grad = None
+        loss = nmce.vocab_parallel_cross_entropy(logits, target, start, end, ctx)
+        loss.backward()
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    timeline: list = []
+    ce_mod.kernel_timeline = timeline
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ce_mod.kernel_timeline = None
+
+    ms_per_step = (t1 - t0) * 1e3 / args.steps
+    per_kernel: dict[str, list[float]] = {}
+    for name, s_ev, e_ev in timeline:
+        per_kernel.setdefault(name, []).append(s_ev.elapsed_time(e_ev))
+    avg_ms = {k: sum(vs) / len(vs) for k, vs in per_kernel.items()}
+
+    slab = n * v * esize
+    alg_bytes = {
+        "nmce_ce_fwd_stats": slab + n * (8 + 12),        # logits read; target in, (m,s,t) out
+        "nmce_ce_bwd": 2 * slab + n * (8 + 8),           # logits read, grad write; target, (M,S)
+    }
+    dominant = max(alg_bytes, key=lambda k: avg_ms.get(k, 0.0))  # one launch each per step
+    achieved = alg_bytes[dominant] / (avg_ms[dominant] * 1e-3) / 1e9
+    step_bytes = 3 * slab + n * 28
+    kernel_ms = sum(avg_ms.values())
+
+    result = {
+        "metric": METRIC,
+        "value": n / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{args.workload}: {wl['desc']}",
+            "tokens": n,
+            "vocab_local": v,
+            "tp": tp,
+            "tp_rank": rank,
+            "logits_dtype": wl["dtype"],
+            "path": "nmce.vocab_parallel_cross_entropy fwd+bwd, in-place grad, target validation",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": achieved,
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": achieved / HBM_PEAK_GBS,
+            "traffic": None,
+            "alg_bytes_per_launch": alg_bytes[dominant],
+            "avg_launch_ms": avg_ms[dominant],
+        },
+        "kernels_ms": avg_ms,
+        "path_roofline": {
+            "alg_bytes_per_step": step_bytes,
+            "kernel_ms_per_step": kernel_ms,
+            "frac_kernels": step_bytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "frac_wall": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        },
+        "device": torch.cuda.get_device_name(0),
+    }
+    del base, logits
+    torch.cuda.empty_cache()
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,122 @@
+/*
+ * nmce.h -- C ABI of the MI355X (gfx950) vocabulary-parallel cross-entropy
+ * library (libnmce.so).
+ *
+ * The library replaces the loss path of nano-megatron:
+ *   nano_megatron/cross_entropy.py:16-85  (_VocabParallelCrossEntropy and
+ *                                           vocab_parallel_cross_entropy)
+ *   nano_megatron/model.py:169-192         (ParallelLMHead, fused variant)
+ *
+ * Conventions shared by every entry point:
+ *   - All tensor pointers are device memory owned by the caller. Unless an
+ *     entry point says otherwise the library never allocates, frees or
+ *     synchronises; work is enqueued on `stream` (a hipStream_t, NULL = the
+ *     legacy default stream).
+ *   - A "row" is one token: the logits of row r start at logits + r*ld
+ *     (elements) and hold `vocab_local` contiguous entries.
+ *   - A shard covers global vocabulary ids [vocab_start, vocab_start+vocab_local).
+ *     Targets are global ids (int64). A target outside the shard contributes
+ *     nothing on that shard (the reference's target_mask, cross_entropy.py:28-36).
+ *   - Return value: NMCE_OK (0), a negative NMCE_E* argument error, or a
+ *     positive hipError_t reported by the launch.
+ */
+#ifndef NMCE_H
+#define NMCE_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types of logits / gradients / hidden states / weights */
+#define NMCE_F32 0
+#define NMCE_BF16 1
+
+/* status codes (negative: argument errors detected before any launch) */
+#define NMCE_OK 0
+#define NMCE_EINVAL_DTYPE (-1)
+#define NMCE_EINVAL_SHAPE (-2)
+#define NMCE_EINVAL_ALIGN (-3)
+#define NMCE_EINVAL_PTR (-4)
+#define NMCE_EINVAL_TP (-5)
+#define NMCE_EINVAL_WORKSPACE (-6)
+
+/* Rows covered by one int32 count of nmce_validate_targets. */
+#define NMCE_VALIDATE_ROWS_PER_SLOT 4096
+
+/* Human-readable text for a status code (static storage). */
+const char* nmce_status_string(int status);
+
+/* Library version, (major << 16) | minor. */
+int nmce_version(void);
+
+/*
+ * Per-shard row statistics, one read pass over the shard's logits.
+ * Replaces cross_entropy.py:21 (row max), :28-36 (masked target pick) and
+ * :40-41 (exp-sum) for one vocabulary shard.
+ *
+ *   row_max[r]    = max_j x[r, j]                         (fp32)
+ *   row_sumexp[r] = sum_j exp(x[r, j] - row_max[r])        (fp32)
+ *   target_logit[r] = x[r, target[r]-vocab_start] if the target is in this
+ *                     shard, else 0.0  (raw logit, not shifted)
+ * dtype: NMCE_F32 or NMCE_BF16 (math is fp32 either way).
+ */
+int nmce_ce_fwd_stats(const void* logits, int dtype, int64_t n_rows,
+                      int64_t vocab_local, int64_t ld, const int64_t* target,
+                      int64_t vocab_start, float* row_max, float* row_sumexp,
+                      float* target_logit, void* stream);
+
+/*
+ * Cross-shard combine of per-shard statistics, done locally.
+ * Replaces the three TP all-reduces and the loss line of cross_entropy.py
+ * (:22-23 MAX, :37-38 SUM of the target logit, :42-43 SUM of exp-sums, :45).
+ *
+ * Shard k's statistic for row r sits at [k*shard_stride + r] of each input
+ * (a [tp, ...] stack, e.g. the all-gathered [tp, 3, n_rows] buffer of a real
+ * TP group with row_max = base, row_sumexp = base + n_rows, target_logit =
+ * base + 2*n_rows and shard_stride = 3*n_rows).
+ *
+ *   g_max[r]    = max_k row_max[k, r]
+ *   g_sumexp[r] = sum_k row_sumexp[k, r] * exp(row_max[k, r] - g_max[r])
+ *   loss[r]     = log(g_sumexp[r]) - (sum_k target_logit[k, r] - g_max[r])
+ * Any of loss / g_max / g_sumexp may be NULL if not wanted.
+ */
+int nmce_ce_combine(const float* row_max, const float* row_sumexp,
+                    const float* target_logit, int tp, int64_t shard_stride,
+                    int64_t n_rows, float* loss, float* g_max, float* g_sumexp,
+                    void* stream);
+
+/*
+ * Target validation (cross_entropy.py:79-81: every target must lie in
+ * [0, vocab_total)). Writes nmce_validate_slots(n_rows) int32 counts of bad
+ * targets, one per NMCE_VALIDATE_ROWS_PER_SLOT rows; every slot is written,
+ * so the buffer needs no clearing. The caller raises if any count is nonzero.
+ */
+int64_t nmce_validate_slots(int64_t n_rows);
+int nmce_validate_targets(const int64_t* target, int64_t n_rows,
+                          int64_t vocab_total, int32_t* bad_counts,
+                          void* stream);
+
+/*
+ * Backward over one shard: grad = (softmax - onehot(target)) * grad_output.
+ * Replaces cross_entropy.py:53-65 plus the autograd cast back to the logits
+ * dtype (the .float() at :83).
+ *
+ *   grad[r, j] = (exp(x[r, j] - g_max[r]) / g_sumexp[r]
+ *                 - [j == target[r] - vocab_start]) * grad_output[r*gout_stride]
+ * gout_stride = 0 broadcasts grad_output[0] to every row (the loss.mean()
+ * case). grad may equal logits (in place, ld_grad == ld); otherwise the two
+ * must not overlap. grad has the same dtype as logits.
+ */
+int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows,
+                int64_t vocab_local, int64_t ld, int64_t ld_grad,
+                const int64_t* target, int64_t vocab_start, const float* g_max,
+                const float* g_sumexp, const float* grad_output,
+                int64_t gout_stride, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NMCE_H */

@@ -1,0 +1,119 @@
+// Device-side helpers shared by the gfx950 kernels of libnmce.
+//
+// Wave64 reductions use DPP (row-local butterflies, then row_bcast15/31 to
+// carry row totals up to lane 63), bf16 is unpacked by shifting into the high
+// half of an fp32, and packed back with the gfx950 instruction
+// v_cvt_pk_bf16_f32 (round to nearest even, NaN-preserving) that clang emits
+// for a float2 -> bf16x2 conversion.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace nmce {
+
+constexpr float kLog2e = 1.4426950408889634f;  // exp(x) = exp2(x * kLog2e)
+constexpr float kNegHuge = -3.402823466e+38f;  // finite floor for running maxima
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float float2_t __attribute__((ext_vector_type(2)));
+// 16 bytes as a native clang vector (what the nontemporal builtins accept).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// v_exp_f32: 2^x, about 1 ulp; 2^-inf = 0.
+__device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even pack of two fp32 into one dword of bf16 (lo, hi).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  float2_t v = {lo, hi};
+  bf16x2_t b = __builtin_convertvector(v, bf16x2_t);
+  return __builtin_bit_cast(uint32_t, b);
+}
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+  return static_cast<uint16_t>(pack_bf16x2(x, 0.0f) & 0xffffu);
+}
+
+// ---- element traits: how a 16-byte vector maps to fp32 values -------------
+template <typename T>
+struct Elem;
+
+template <>
+struct Elem<float> {
+  static constexpr int kPerVec = 4;
+  __device__ static __forceinline__ void unpack(const u32x4& v, float* f) {
+    f[0] = __uint_as_float(v.x);
+    f[1] = __uint_as_float(v.y);
+    f[2] = __uint_as_float(v.z);
+    f[3] = __uint_as_float(v.w);
+  }
+  __device__ static __forceinline__ u32x4 pack(const float* f) {
+    return u32x4{__float_as_uint(f[0]), __float_as_uint(f[1]), __float_as_uint(f[2]),
+                 __float_as_uint(f[3])};
+  }
+  __device__ static __forceinline__ float load1(const float* p) { return *p; }
+  __device__ static __forceinline__ void store1(float* p, float v) { *p = v; }
+};
+
+template <>
+struct Elem<uint16_t> {  // bf16 storage
+  static constexpr int kPerVec = 8;
+  __device__ static __forceinline__ void unpack(const u32x4& v, float* f) {
+    f[0] = bf16_lo(v.x); f[1] = bf16_hi(v.x);
+    f[2] = bf16_lo(v.y); f[3] = bf16_hi(v.y);
+    f[4] = bf16_lo(v.z); f[5] = bf16_hi(v.z);
+    f[6] = bf16_lo(v.w); f[7] = bf16_hi(v.w);
+  }
+  __device__ static __forceinline__ u32x4 pack(const float* f) {
+    return u32x4{pack_bf16x2(f[0], f[1]), pack_bf16x2(f[2], f[3]), pack_bf16x2(f[4], f[5]),
+                 pack_bf16x2(f[6], f[7])};
+  }
+  __device__ static __forceinline__ float load1(const uint16_t* p) { return bf16_to_f32(*p); }
+  __device__ static __forceinline__ void store1(uint16_t* p, float v) { *p = f32_to_bf16(v); }
+};
+
+// Streaming 16-byte loads: the logit slab is read once per pass and is far
+// larger than L2 + MALL, so mark the loads non-temporal.
+__device__ __forceinline__ u32x4 load_stream(const u32x4* p) {
+  return __builtin_nontemporal_load(p);
+}
+__device__ __forceinline__ void store_stream(u32x4* p, const u32x4& v) {
+  __builtin_nontemporal_store(v, p);
+}
+
+// ---- wave64 reductions via DPP ---------------------------------------------
+// DPP controls (GFX9): quad_perm, row_half_mirror 0x141, row_mirror 0x140,
+// row_bcast:15 0x142, row_bcast:31 0x143.
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_f(float old, float v) {
+  return __builtin_amdgcn_update_dpp(old, v, kCtrl, kRowMask, 0xf, false);
+}
+
+// Reductions over the 64 lanes of a wave; every lane must be active. The
+// result is returned uniformly (read from lane 63).
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f<0xB1, 0xf>(0.0f, v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E, 0xf>(0.0f, v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141, 0xf>(0.0f, v);  // row_half_mirror
+  v += dpp_f<0x140, 0xf>(0.0f, v);  // row_mirror: every lane holds its row sum
+  v += dpp_f<0x142, 0xa>(0.0f, v);  // row_bcast:15 into rows 1 and 3
+  v += dpp_f<0x143, 0xc>(0.0f, v);  // row_bcast:31 into rows 2 and 3
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f<0xB1, 0xf>(kNegHuge, v));
+  v = fmaxf(v, dpp_f<0x4E, 0xf>(kNegHuge, v));
+  v = fmaxf(v, dpp_f<0x141, 0xf>(kNegHuge, v));
+  v = fmaxf(v, dpp_f<0x140, 0xf>(kNegHuge, v));
+  v = fmaxf(v, dpp_f<0x142, 0xa>(kNegHuge, v));
+  v = fmaxf(v, dpp_f<0x143, 0xc>(kNegHuge, v));
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+}  // namespace nmce

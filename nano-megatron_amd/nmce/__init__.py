@@ -1,0 +1,29 @@
+"""nmce: nano-megatron's vocabulary-parallel cross entropy on MI355X (gfx950).
+
+Public API (mirrors nano_megatron/cross_entropy.py and parallel.py):
+
+* ``vocab_parallel_cross_entropy(logits, target, vocab_start, vocab_end, ctx)``
+  -> mean fp32 loss; backward yields the logits gradient.
+* ``_VocabParallelCrossEntropy`` -- the autograd Function (per-token loss).
+* ``ParallelContext`` / ``vocab_range`` / ``divide`` -- the topology fields and
+  shard rule the loss reads.
+
+All compute runs in ``libnmce.so`` (hand-written HIP for gfx950) through the C
+ABI in ``include/nmce.h``; there is no CPU or PyTorch fallback.
+"""
+
+from .cross_entropy import (
+    _VocabParallelCrossEntropy,
+    validate_targets,
+    vocab_parallel_cross_entropy,
+)
+from .parallel import ParallelContext, divide, vocab_range
+
+__all__ = [
+    "_VocabParallelCrossEntropy",
+    "ParallelContext",
+    "divide",
+    "validate_targets",
+    "vocab_parallel_cross_entropy",
+    "vocab_range",
+]

@@ -1,0 +1,89 @@
+"""ctypes binding of ``libnmce.so`` (declared in ``include/nmce.h``).
+
+The library is loaded after ``import torch`` so that its ``libamdhip64.so.7``
+dependency resolves to the HIP runtime torch already mapped: both then share
+one runtime, one device context and torch's streams.
+
+There is no fallback: if the library is missing or a call fails, the caller
+gets an exception.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import pathlib
+import threading
+
+import torch  # noqa: F401  (must be imported before the HIP library is loaded)
+
+LIB_PATH = pathlib.Path(__file__).resolve().parent / "libnmce.so"
+
+NMCE_F32 = 0
+NMCE_BF16 = 1
+NMCE_VALIDATE_ROWS_PER_SLOT = 4096
+
+_c_int = ctypes.c_int
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+
+# name -> (restype, argtypes), mirroring include/nmce.h
+SIGNATURES: dict[str, tuple] = {
+    "nmce_status_string": (ctypes.c_char_p, [_c_int]),
+    "nmce_version": (_c_int, []),
+    "nmce_ce_fwd_stats": (_c_int, [_p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p]),
+    "nmce_ce_combine": (_c_int, [_p, _p, _p, _c_int, _i64, _i64, _p, _p, _p, _p]),
+    "nmce_validate_slots": (_i64, [_i64]),
+    "nmce_validate_targets": (_c_int, [_p, _i64, _i64, _p, _p]),
+    "nmce_ce_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _p]),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+class NmceError(RuntimeError):
+    """A libnmce entry point returned a nonzero status."""
+
+
+def load() -> ctypes.CDLL:
+    """Load and type the library once per process."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise NmceError(
+                    f"{LIB_PATH} is not built; run `python -m nmce._build` in "
+                    "nano-megatron_amd/ (or __graft_entry__.build())"
+                )
+            lib = ctypes.CDLL(str(LIB_PATH))
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def check(status: int, what: str) -> None:
+    if status != 0:
+        msg = load().nmce_status_string(status).decode()
+        raise NmceError(f"{what} failed with status {status}: {msg}")
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return NMCE_F32
+    if dtype == torch.bfloat16:
+        return NMCE_BF16
+    raise TypeError(f"unsupported logits dtype {dtype}; expected float32 or bfloat16")
+
+
+def stream_handle(device: torch.device) -> int:
+    """The raw hipStream_t of torch's current stream on ``device``."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

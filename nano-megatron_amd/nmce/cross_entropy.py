@@ -1,0 +1,234 @@
+"""Cross entropy over a vocabulary-sharded logit slab, on gfx950 HIP kernels.
+
+Drop-in for nano_megatron/cross_entropy.py:16-85. Same names, same arguments,
+same returned loss (per-token fp32 from the Function, its mean from the
+wrapper), same ``ValueError`` for a target outside the vocabulary.
+
+Differences from the reference, all deliberate:
+
+* bf16 logits are consumed directly. The reference upcasts them with
+  ``.float()`` (cross_entropy.py:83) and autograd casts the fp32 gradient
+  back; here the math is fp32 in registers and the gradient is written once,
+  in the logits dtype.
+* Nothing of size ``[tokens, vocab]`` is kept between forward and backward:
+  the reference saves the fp32 softmax (:48-49); this keeps two floats per
+  token (row max, row exp-sum) and recomputes the softmax in backward from the
+  logits.
+* By default the gradient is written **in place** into the logits storage
+  when the logits are a non-leaf tensor (as at model.py:277-281, where they
+  come straight from the LM-head matmul, which does not save them). Pass
+  ``inplace=False`` to keep the logits intact; leaf tensors are never
+  overwritten. The version counter of the logits is bumped after an in-place
+  write, so any other autograd node that saved them fails loudly instead of
+  reading gradients.
+* With ``tp_size > 1`` the three dependent all-reduces (:23, :38, :43) become
+  one all-gather of packed ``[3, tokens]`` statistics followed by a local
+  combine.
+
+There is no CPU path: the tensors must be on a ROCm device and ``libnmce.so``
+must be built; anything else raises.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.distributed as dist
+
+from . import _lib
+
+# Optional launch timeline. When set to a list, every kernel launch of this
+# module appends (name, start_event, end_event), both recorded on the launch
+# stream, so a caller can time each kernel inside a running workload.
+kernel_timeline: list | None = None
+
+
+def _launch(name: str, fn, *args) -> None:
+    timeline = kernel_timeline
+    if timeline is None:
+        _lib.check(fn(*args), name)
+        return
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    status = fn(*args)
+    end.record()
+    timeline.append((name, start, end))
+    _lib.check(status, name)
+
+
+def _as_rows(logits: torch.Tensor) -> torch.Tensor | None:
+    """``[..., V]`` -> ``[rows, V]`` view sharing storage, or None if not viewable."""
+    if logits.dim() == 0 or logits.stride(-1) != 1:
+        return None
+    try:
+        return logits.view(-1, logits.shape[-1])
+    except RuntimeError:
+        return None
+
+
+def _check_inputs(logits: torch.Tensor, target: torch.Tensor, vocab_start: int,
+                  vocab_end: int) -> None:
+    if not logits.is_cuda:
+        raise RuntimeError("nmce: logits must be on a ROCm device (there is no CPU path)")
+    if target.device != logits.device:
+        raise RuntimeError(f"nmce: target on {target.device}, logits on {logits.device}")
+    if target.dtype != torch.int64:
+        raise TypeError(f"nmce: target must be int64, got {target.dtype}")
+    _lib.dtype_code(logits.dtype)
+    if tuple(target.shape) != tuple(logits.shape[:-1]):
+        raise ValueError(
+            f"nmce: target shape {tuple(target.shape)} does not match logits "
+            f"{tuple(logits.shape)} without the vocabulary dimension")
+    if vocab_end - vocab_start != logits.shape[-1]:
+        raise ValueError(
+            f"nmce: logits hold {logits.shape[-1]} vocabulary entries but the shard "
+            f"[{vocab_start}, {vocab_end}) has {vocab_end - vocab_start}")
+
+
+def validate_targets(target: torch.Tensor, vocab_size: int) -> None:
+    """Raise ``ValueError`` if any target is outside ``[0, vocab_size)``.
+
+    Same check and message as cross_entropy.py:79-81, run as one kernel and
+    one small device-to-host read (the reference uses two ``torch.any``
+    reductions, each a host sync).
+    """
+    lib = _lib.load()
+    t = target.reshape(-1)
+    if not t.is_contiguous():
+        t = t.contiguous()
+    n = t.numel()
+    if n == 0:
+        return
+    slots = lib.nmce_validate_slots(n)
+    counts = torch.empty(slots, dtype=torch.int32, device=t.device)
+    _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n, vocab_size,
+            counts.data_ptr(), _lib.stream_handle(t.device))
+    if int(counts.cpu().sum()) != 0:
+        raise ValueError("target token id is outside the model vocabulary")
+
+
+def _exchange_stats(local: torch.Tensor, group, world_size: int) -> torch.Tensor:
+    """All-gather the packed ``[3, rows]`` statistics of every TP rank.
+
+    One collective of 12 bytes per token instead of the reference's three
+    dependent all-reduces (cross_entropy.py:23, :38, :43).
+    """
+    gathered = torch.empty((world_size,) + tuple(local.shape), dtype=local.dtype,
+                           device=local.device)
+    dist.all_gather_into_tensor(gathered, local, group=group)
+    return gathered
+
+
+class _VocabParallelCrossEntropy(torch.autograd.Function):
+    """Per-token loss over a vocabulary shard (cross_entropy.py:16-65).
+
+    ``forward(logits, target, vocab_start, vocab_end, group, world_size,
+    inplace=None)`` returns the per-token fp32 loss with ``target``'s shape;
+    ``backward`` returns the logits gradient in the logits dtype.
+    """
+
+    @staticmethod
+    def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None):
+        _check_inputs(logits, target, vocab_start, vocab_end)
+        lib = _lib.load()
+        dev = logits.device
+        stream = _lib.stream_handle(dev)
+        V = logits.shape[-1]
+
+        rows = _as_rows(logits)
+        if inplace is None:
+            inplace = logits.grad_fn is not None
+        elif inplace and logits.grad_fn is None and logits.requires_grad:
+            raise ValueError("nmce: refusing to write the gradient into a leaf tensor; "
+                             "pass inplace=False or None")
+        if rows is None:  # not viewable as [rows, V]: work on a contiguous copy
+            rows = logits.contiguous().view(-1, V)
+            inplace = False
+        n = rows.shape[0]
+        ld = rows.stride(0) if n > 1 else V
+        tgt = target.reshape(-1)
+        if not tgt.is_contiguous():
+            tgt = tgt.contiguous()
+
+        local = torch.empty((3, n), dtype=torch.float32, device=dev)
+        _launch("nmce_ce_fwd_stats", lib.nmce_ce_fwd_stats,
+                rows.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ld, tgt.data_ptr(),
+                vocab_start, local[0].data_ptr(), local[1].data_ptr(), local[2].data_ptr(), stream)
+
+        if world_size > 1:
+            stats = _exchange_stats(local, group, world_size)
+        else:
+            stats = local
+        loss = torch.empty(n, dtype=torch.float32, device=dev)
+        row_stat = torch.empty((2, n), dtype=torch.float32, device=dev)  # global max, exp-sum
+        _launch("nmce_ce_combine", lib.nmce_ce_combine,
+                stats.data_ptr(), stats.data_ptr() + 4 * n, stats.data_ptr() + 8 * n, world_size,
+                3 * n, n, loss.data_ptr(), row_stat[0].data_ptr(), row_stat[1].data_ptr(), stream)
+
+        ctx.inplace = bool(inplace)
+        ctx.vocab_start = vocab_start
+        ctx.logits_shape = logits.shape
+        ctx.ld = ld
+        # `rows` aliases `logits` unless a contiguous copy was made above.
+        ctx.save_for_backward(rows, tgt, row_stat, logits if ctx.inplace else None)
+        return loss.view(target.shape)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        rows, tgt, row_stat, original = ctx.saved_tensors
+        lib = _lib.load()
+        n, V = rows.shape
+        go = grad_output
+        if go.dtype != torch.float32:
+            go = go.float()
+        if go.numel() > 0 and all(s == 0 for s in go.stride()):
+            gstride = 0  # expanded scalar, e.g. from loss.mean()
+        else:
+            go = go.reshape(-1)
+            if not go.is_contiguous():
+                go = go.contiguous()
+            gstride = 1
+        if ctx.inplace:
+            out = rows
+            ld_out = ctx.ld
+        else:
+            out = torch.empty((n, V), dtype=rows.dtype, device=rows.device)
+            ld_out = V
+        _launch("nmce_ce_bwd", lib.nmce_ce_bwd,
+                rows.data_ptr(), out.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, ld_out,
+                tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
+                go.data_ptr(), gstride, _lib.stream_handle(rows.device))
+        if ctx.inplace:
+            # The logits now hold the gradient: make later readers that saved
+            # them fail their version check.
+            torch.autograd.graph.increment_version(original)
+            grad = original.detach()
+        else:
+            grad = out.view(ctx.logits_shape)
+        return grad, None, None, None, None, None, None
+
+
+def vocab_parallel_cross_entropy(
+    logits: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    ctx,
+    *,
+    inplace: bool | None = None,
+    validate: bool = True,
+) -> torch.Tensor:
+    """Mean cross-entropy loss from vocab-sharded ``logits`` (cross_entropy.py:68-85).
+
+    ``logits`` is ``[b, s, V/tp]`` (fp32 or bf16); ``target`` is ``[b, s]`` of
+    global token ids; ``ctx`` provides ``tp_size`` and ``tp_group``. Returns a
+    0-dim fp32 tensor. ``validate=False`` skips the host-synchronising target
+    check (the kernels never read out of bounds either way).
+    """
+    _check_inputs(logits, target, vocab_start, vocab_end)
+    vocab_size = ctx.tp_size * (vocab_end - vocab_start)
+    if validate:
+        validate_targets(target, vocab_size)
+    loss = _VocabParallelCrossEntropy.apply(
+        logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace)
+    return loss.mean()

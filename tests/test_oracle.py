@@ -1,0 +1,220 @@
+"""Pins the CPU oracle (oracle/) before anything is compared against it.
+
+Checks, each chosen so a plausible mistake fails at least one of them:
+* golden vectors from fp64 ``F.cross_entropy`` (tests/golden/make_golden.py),
+  including the reference's own check shape [2,5,16] seed 0 at tp in {2,4}
+  (nano-megatron tests/check_tp_math.py:94-158) and the c1 workload;
+* brute force: per-shard stats + combine on the concatenated slab equal the
+  full-vocabulary closed form; shard gradients are column slices of the full
+  gradient;
+* invariants: shift invariance, full-vocab gradient rows sum to 0, loss >= 0,
+  constant rows give log V, V = 1 gives loss 0 and gradient 0;
+* planted mistakes: mutated copies of the oracle (missing target mask,
+  off-by-one shard offset, combine without rescale, onehot with the wrong
+  sign, a dropped max shift) must fail these checks.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from _util import assert_close_rel, c1_inputs, load_json, load_npz, sha256_of
+from oracle import ce_oracle as O
+from oracle import ce_restate as R
+
+# ---------------------------------------------------------------- check bodies
+
+
+def check_tp_math(sharded=O.sharded, closed=O.closed_form):
+    gold = load_npz("tp_math_2x5x16.npz")
+    x = gold["logits"].reshape(10, 16)
+    t = gold["target"].ravel()
+    loss, grad = closed(x, t, 1.0 / 10)
+    assert_close_rel(loss, gold["loss"], 1e-12, what="closed-form loss")
+    assert_close_rel(loss.mean(), gold["mean"], 1e-12, what="closed-form mean")
+    assert_close_rel(grad, gold["grad_mean"], 1e-12, 1e-15, what="closed-form grad")
+    for tp in (2, 4):
+        l, grads, _, _ = sharded(x, t, tp, 1.0 / 10)
+        assert_close_rel(l, gold["loss"], 1e-12, what=f"tp={tp} loss")
+        assert_close_rel(np.concatenate(grads, 1), gold["grad_mean"], 1e-12, 1e-15,
+                         what=f"tp={tp} grad")
+
+
+def check_shard_pairs(sharded=O.sharded):
+    for name in ("shard_pair_f32.npz", "shard_pair_bf16.npz"):
+        gold = load_npz(name)
+        l, grads, _, _ = sharded(gold["logits"], gold["target"], int(gold["tp"]))
+        assert_close_rel(l, gold["loss"], 1e-12, what=f"{name} loss")
+        assert_close_rel(np.concatenate(grads, 1), gold["grad_sum"], 1e-6, 1e-12,
+                         what=f"{name} grad")
+
+
+def check_edge_rows(closed=O.closed_form):
+    gold = load_npz("edge_rows.npz")
+    l, g = closed(gold["logits"], gold["target"])
+    assert_close_rel(l, gold["loss"], 1e-12, 1e-14, what="edge loss")
+    assert_close_rel(g, gold["grad_sum"], 1e-12, 1e-15, what="edge grad")
+
+
+def check_brute_force(sharded=O.sharded, closed=O.closed_form):
+    rng = np.random.default_rng(1)
+    for tp, (n, v) in ((2, (7, 64)), (4, (5, 128)), (3, (6, 99))):
+        x = rng.normal(0, 3, (n, v))
+        t = rng.integers(0, v, n)
+        t[0], t[-1] = 0, v - 1
+        fl, fg = closed(x, t)
+        sl, sg, _, _ = sharded(x, t, tp)
+        assert_close_rel(sl, fl, 1e-12, 1e-14, what=f"tp={tp} sharded vs closed loss")
+        assert_close_rel(np.concatenate(sg, 1), fg, 1e-12, 1e-15, what=f"tp={tp} grad")
+
+
+# ------------------------------------------------------------------- the tests
+
+
+def test_oracle_tp_math_golden():
+    check_tp_math()
+
+
+def test_oracle_shard_pair_golden():
+    check_shard_pairs()
+
+
+def test_oracle_edge_rows_golden():
+    check_edge_rows()
+
+
+def test_oracle_brute_force_sharding():
+    check_brute_force()
+
+
+def test_oracle_c1_golden():
+    """The c1 workload (fp32 [4,256,32000] ~ N(0,2^2), seed 0) in full."""
+    gold = load_json("c1_digest.json")
+    x, t = c1_inputs()
+    assert sha256_of(x, t) == gold["sha256_inputs"]
+    loss, grad = O.closed_form(x.reshape(1024, 32000).numpy(), t.reshape(-1).numpy(), 1 / 1024)
+    assert_close_rel(loss, gold["loss"], 1e-12, what="c1 loss")
+    assert_close_rel(loss.mean(), gold["mean"], 1e-12, what="c1 mean")
+    got = grad[np.array(gold["grad_rows"]), np.array(gold["grad_cols"])]
+    assert_close_rel(got, gold["grad_vals"], 1e-10, 1e-18, what="c1 grad")
+
+
+def test_oracle_invariants():
+    rng = np.random.default_rng(2)
+    x = rng.normal(0, 2, (6, 50))
+    t = rng.integers(0, 50, 6)
+    l, g = O.closed_form(x, t)
+    assert (l >= 0).all()
+    assert np.allclose(g.sum(1), 0.0, atol=1e-14)
+    l2, g2 = O.closed_form(x + rng.normal(0, 10, (6, 1)), t)  # per-row shift
+    assert np.allclose(l, l2, rtol=1e-12, atol=1e-12) and np.allclose(g, g2, atol=1e-14)
+    lc, _ = O.closed_form(np.full((3, 77), 1.5), np.array([0, 5, 76]))
+    assert np.allclose(lc, np.log(77), rtol=1e-14)
+    l1, g1 = O.closed_form(np.array([[4.0], [-2.0]]), np.array([0, 0]))
+    assert np.all(l1 == 0) and np.all(g1 == 0)
+    ld, _ = O.closed_form(np.array([[50.0] + [0.0] * 9]), np.array([0]))
+    assert ld[0] < 1e-20
+
+
+def test_restatement_matches_golden():
+    """The torch-CPU op-sequence restatement (the timed CPU baseline) agrees
+    with F.cross_entropy fp64 at fp32 accuracy, at TP=1 and as rank 1 of a
+    TP=2 pair whose peer partials are fed through the emulated all-reduce."""
+    gold = load_npz("tp_math_2x5x16.npz")
+    x = torch.from_numpy(gold["logits"])
+    t = torch.from_numpy(gold["target"])
+    loss, saved = R.forward(x, t, 0, 16)
+    assert loss.dtype == torch.float32
+    assert_close_rel(loss.numpy().ravel(), gold["loss"], 1e-6, what="restated loss")
+    g = R.backward(saved, torch.full((2, 5), 0.1))
+    assert_close_rel(g.numpy().reshape(10, 16), gold["grad_mean"], 1e-5, 1e-9,
+                     what="restated grad")
+
+    gold = load_npz("shard_pair_bf16.npz")
+    full = torch.from_numpy(gold["logits"]).to(torch.bfloat16)
+    t = torch.from_numpy(gold["target"])
+    mine, peer = full[:, 512:], full[:, :512]
+    gmax = torch.maximum(mine.float().max(-1)[0], peer.float().max(-1)[0])
+    pick, psum = R.peer_partials(peer, t, 0, 512, gmax)
+    hook = R.fixed_peer_all_reduce(peer.float().max(-1)[0], pick, psum)
+    loss, saved = R.forward(mine, t, 512, 1024, all_reduce=hook)
+    assert_close_rel(loss.numpy(), gold["loss"], 1e-6, what="rank-1 loss")
+    g = R.backward(saved, torch.ones(16))
+    assert g.dtype == torch.bfloat16
+    assert_close_rel(g.float().numpy(), gold["grad_sum"][:, 512:], 2 ** -8, 1e-30,
+                     what="rank-1 bf16 grad")
+
+
+# ------------------------------------------------------------ planted mistakes
+
+
+def _mut_stats_no_mask(x_shard, target, vocab_start):
+    x = np.asarray(x_shard, dtype=np.float64)
+    n, v = x.shape
+    m = x.max(1)
+    s = np.exp(x - m[:, None]).sum(1)
+    local = np.clip(np.asarray(target) - vocab_start, 0, v - 1)
+    return m, s, x[np.arange(n), local]  # forgets to zero unowned picks
+
+
+def _mut_stats_offset(x_shard, target, vocab_start):
+    return O.shard_stats(x_shard, target, vocab_start + 1)
+
+
+def _mut_combine_no_rescale(stats):
+    M = np.stack([st[0] for st in stats]).max(0)
+    S = sum(st[1] for st in stats)
+    xt = sum(st[2] for st in stats)
+    return M, S, np.log(S) - (xt - M)
+
+
+def _sharded_with(stats_fn=O.shard_stats, combine_fn=O.combine, grad_fn=O.shard_grad):
+    def run(x_full, target, tp, grad_output=None):
+        n, vfull = x_full.shape
+        per = vfull // tp
+        shards = [x_full[:, r * per:(r + 1) * per] for r in range(tp)]
+        stats = [stats_fn(sh, target, r * per) for r, sh in enumerate(shards)]
+        M, S, loss = combine_fn(stats)
+        grads = [grad_fn(sh, target, r * per, M, S, grad_output) for r, sh in enumerate(shards)]
+        return loss, grads, M, S
+    return run
+
+
+def _mut_grad_sign(x_shard, target, vocab_start, M, S, grad_output=None):
+    g = O.shard_grad(x_shard, target, vocab_start, M, S, None)
+    local = np.asarray(target) - vocab_start
+    owned = (local >= 0) & (local < g.shape[1])
+    rows = np.nonzero(owned)[0]
+    g[rows, local[rows]] += 2.0  # onehot added instead of subtracted
+    go = 1.0 if grad_output is None else np.asarray(grad_output)
+    return g * (go if np.ndim(go) == 0 else go[:, None])
+
+
+def _mut_closed_no_shift(x, target, grad_output=None):
+    x = np.asarray(x, dtype=np.float32)  # fp32 with no max shift overflows
+    e = np.exp(x)
+    s = e.sum(1, dtype=np.float32)
+    loss = np.log(s) - x[np.arange(x.shape[0]), target]
+    g = e / s[:, None]
+    g[np.arange(x.shape[0]), target] -= 1
+    go = 1.0 if grad_output is None else grad_output
+    return loss.astype(np.float64), g.astype(np.float64) * go
+
+
+@pytest.mark.parametrize("mutant,check", [
+    (_sharded_with(stats_fn=_mut_stats_no_mask), check_tp_math),
+    (_sharded_with(stats_fn=_mut_stats_offset), check_shard_pairs),
+    (_sharded_with(combine_fn=_mut_combine_no_rescale), check_brute_force),
+    (_sharded_with(grad_fn=_mut_grad_sign), check_shard_pairs),
+])
+def test_planted_mistakes_in_sharding_are_caught(mutant, check):
+    with pytest.raises(AssertionError):
+        check(sharded=mutant)
+
+
+def test_planted_dropped_shift_is_caught():
+    with np.errstate(over="ignore", invalid="ignore"):
+        with pytest.raises(AssertionError):
+            check_edge_rows(closed=_mut_closed_no_shift)
