@@ -67,6 +67,26 @@ def parse_args():
     return p.parse_args()
 
 
+def lm_head_stand_in():
+    """An autograd node standing where the LM-head matmul is (model.py:192):
+    forward hands the resident logits on as a non-leaf tensor, backward
+    receives d(logits) and stops there (the dX/dW GEMMs that would consume it
+    are not part of the loss path). Without it the logits would be a leaf and
+    autograd would copy the whole gradient into ``.grad`` each step."""
+    import torch
+
+    class LMHeadOutput(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, logits, anchor):
+            return logits.view_as(logits)
+
+        @staticmethod
+        def backward(ctx, dlogits):
+            return None, None
+
+    return LMHeadOutput
+
+
 def host_cpu_model() -> str:
     try:
         for line in open("/proc/cpuinfo"):
@@ -175,13 +195,14 @@ def main() -> int:
 
         ce_mod._exchange_stats = emulated_all_gather
 
-    # Non-leaf logits on the same storage (a view of a leaf), as the LM-head
-    # output is at model.py:277: the gradient goes in place.
-    base.requires_grad_(True)
-    logits = base.view(wl["b"], wl["s"], v)
+    # Non-leaf logits produced by an LM-head node, as at model.py:277: the
+    # gradient goes in place into the logits storage.
+    anchor = torch.zeros((), device=dev, requires_grad=True)
+    lm_head = lm_head_stand_in()
+    slab = base.view(wl["b"], wl["s"], v)
 
     def step():
-        base.grad = None
+        logits = lm_head.apply(slab, anchor)
         loss = nmce.vocab_parallel_cross_entropy(logits, target, start, end, ctx)
         loss.backward()
         return loss
@@ -257,7 +278,7 @@ def main() -> int:
         },
         "device": torch.cuda.get_device_name(0),
     }
-    del base, logits
+    del base, slab
     torch.cuda.empty_cache()
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)

@@ -43,7 +43,7 @@ extern "C" {
 #define NMCE_EINVAL_WORKSPACE (-6)
 
 /* Rows covered by one int32 count of nmce_validate_targets. */
-#define NMCE_VALIDATE_ROWS_PER_SLOT 4096
+#define NMCE_VALIDATE_ROWS_PER_SLOT 1024
 
 /* Human-readable text for a status code (static storage). */
 const char* nmce_status_string(int status);
@@ -66,6 +66,17 @@ int nmce_ce_fwd_stats(const void* logits, int dtype, int64_t n_rows,
                       int64_t vocab_local, int64_t ld, const int64_t* target,
                       int64_t vocab_start, float* row_max, float* row_sumexp,
                       float* target_logit, void* stream);
+
+/*
+ * Single-shard forward (TP=1): the statistics pass with the combine folded
+ * in. Same results as nmce_ce_fwd_stats(vocab_start = 0) followed by
+ * nmce_ce_combine(tp = 1), bit for bit, in one read pass and one launch.
+ * Replaces cross_entropy.py:17-50 at world_size == 1.
+ *   g_max[r], g_sumexp[r], loss[r] as defined for nmce_ce_combine.
+ */
+int nmce_ce_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
+                int64_t ld, const int64_t* target, float* loss, float* g_max,
+                float* g_sumexp, void* stream);
 
 /*
  * Cross-shard combine of per-shard statistics, done locally.

@@ -9,11 +9,17 @@
 //                     grad_output, written in the logits dtype, optionally in
 //                     place (:53-65 plus the cast back of :83)
 //
-// Layout: one workgroup per row (token). A row of the c2 workload is 50304
-// bf16 = 98 KiB, so a 256-lane workgroup streams it with 16-byte
-// non-temporal loads, UNROLL of them in flight per lane. Per-lane partial
-// (max, sumexp) pairs are merged with DPP inside each wave and through LDS
-// across the waves of the workgroup.
+// Forward layout: one 1024-lane workgroup per row (token). A row of 50304
+// bf16 is 98 KiB; the workgroup streams it with 16-byte non-temporal loads,
+// four in flight per lane, folding them into per-lane (max, sumexp) pairs that
+// are merged with DPP inside each wave and through LDS across the 16 waves.
+// Big workgroups keep fewer rows open at once (512 on 256 CUs), which keeps
+// the HBM access stream close to sequential.
+//
+// Backward layout: when rows are 16-byte aligned and the width is a multiple
+// of the vector, the slab's vectors are numbered row-major and dealt out like
+// a copy kernel (ce_bwd_flat_kernel), so the resident workgroups sweep one
+// contiguous window of HBM; otherwise one workgroup per row (ce_bwd_kernel).
 #include <float.h>
 #include <hip/hip_runtime.h>
 
@@ -23,8 +29,13 @@
 namespace nmce {
 namespace {
 
-constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+constexpr int kStatsBlock = 1024;
+constexpr int kStatsUnroll = 4;
+constexpr int kBwdBlock = 1024;   // row-per-workgroup backward
+constexpr int kBwdUnroll = 4;
+constexpr int kFlatBlock = 256;   // flat backward
+constexpr int kFlatUnroll = 2;
+constexpr int kValidateThreads = 256;
 // Running maxima start here instead of -inf so that rows (or lanes) that have
 // seen only -inf keep finite shifts and 2^(x-m) stays 0 rather than NaN.
 constexpr float kMaxFloor = -1.0e38f;
@@ -57,11 +68,15 @@ __device__ __forceinline__ int64_t head_elems(const T* p, int64_t v) {
   return h < v ? h : v;
 }
 
-template <typename T>
+// kFinal = false: per-shard statistics (out0 = row max, out1 = row exp-sum,
+//                  out2 = raw target logit or 0 when the shard does not own it).
+// kFinal = true:  the shard is the whole vocabulary (TP=1), so the combine is
+//                  folded in: out0 = max, out1 = exp-sum, out2 = per-token loss.
+template <typename T, bool kFinal, int kBlock = kStatsBlock, int kUnroll = kStatsUnroll>
 __global__ __launch_bounds__(kBlock) void ce_stats_kernel(
     const T* __restrict__ x, int64_t n_rows, int64_t V, int64_t ld,
-    const int64_t* __restrict__ target, int64_t vstart, float* __restrict__ out_m,
-    float* __restrict__ out_s, float* __restrict__ out_t) {
+    const int64_t* __restrict__ target, int64_t vstart, float* __restrict__ out0,
+    float* __restrict__ out1, float* __restrict__ out2) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
   constexpr int kWaves = kBlock / 64;
@@ -120,10 +135,12 @@ __global__ __launch_bounds__(kBlock) void ce_stats_kernel(
       float S = 0.0f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) S += sm_s[w] * exp2_hw((sm_m[w] - M) * kLog2e);
-      out_m[row] = M;
-      out_s[row] = S;
       const int64_t lt = target[row] - vstart;
-      out_t[row] = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
+      const float xt = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
+      out0[row] = M;
+      out1[row] = S;
+      // Same association as the reference: log(sum) - (x_t - max).
+      out2[row] = kFinal ? logf(S) - (xt - M) : xt;
     }
     __syncthreads();
   }
@@ -151,21 +168,31 @@ __global__ __launch_bounds__(256) void ce_combine_kernel(
 // Count of targets outside [0, vocab_total) per slot of
 // NMCE_VALIDATE_ROWS_PER_SLOT rows. Every block writes its own slot, so the
 // output needs no clearing.
-__global__ __launch_bounds__(256) void validate_targets_kernel(
+__global__ __launch_bounds__(kValidateThreads) void validate_targets_kernel(
     const int64_t* __restrict__ target, int64_t n_rows, int64_t vocab_total,
     int32_t* __restrict__ bad_counts) {
-  __shared__ int32_t sm_bad[4];
+  static_assert(NMCE_VALIDATE_ROWS_PER_SLOT % kValidateThreads == 0, "slot size");
+  constexpr int kPerThread = NMCE_VALIDATE_ROWS_PER_SLOT / kValidateThreads;
+  __shared__ int32_t sm_bad[kValidateThreads / 64];
   const int64_t base = static_cast<int64_t>(blockIdx.x) * NMCE_VALIDATE_ROWS_PER_SLOT;
   int bad = 0;
-  for (int64_t r = base + threadIdx.x; r < n_rows && r < base + NMCE_VALIDATE_ROWS_PER_SLOT;
-       r += 256) {
-    const int64_t tg = target[r];
-    bad += (tg < 0 || tg >= vocab_total) ? 1 : 0;
+#pragma unroll
+  for (int k = 0; k < kPerThread; ++k) {
+    const int64_t r = base + k * kValidateThreads + threadIdx.x;
+    if (r < n_rows) {
+      const int64_t tg = target[r];
+      bad += (tg < 0 || tg >= vocab_total) ? 1 : 0;
+    }
   }
   bad = static_cast<int>(wave_sum(static_cast<float>(bad)));
   if ((threadIdx.x & 63) == 0) sm_bad[threadIdx.x >> 6] = bad;
   __syncthreads();
-  if (threadIdx.x == 0) bad_counts[blockIdx.x] = sm_bad[0] + sm_bad[1] + sm_bad[2] + sm_bad[3];
+  if (threadIdx.x == 0) {
+    int total = 0;
+#pragma unroll
+    for (int w = 0; w < kValidateThreads / 64; ++w) total += sm_bad[w];
+    bad_counts[blockIdx.x] = total;
+  }
 }
 
 // grad = (exp(x - M) / S - onehot) * g for one element; the onehot column
@@ -174,7 +201,7 @@ __device__ __forceinline__ float target_grad(float x, float mc, float S, float g
   return (exp2_hw(fmaf(x, kLog2e, -mc)) / S - 1.0f) * g;
 }
 
-template <typename T, bool kVec>
+template <typename T, bool kVec, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
 __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
@@ -250,6 +277,53 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
   }
 }
 
+// Flat backward. Vector f of the slab is (row, j) = (f / vpr, f % vpr), with
+// vpr = V / EPV vectors per row; workgroup b takes vectors
+// [b*kBlock*kUnroll, (b+1)*kBlock*kUnroll). Preconditions (checked by the
+// host): V % EPV == 0, logits and grad rows 16-byte aligned, n*vpr < 2^31.
+// The arithmetic per element is exactly that of ce_bwd_kernel.
+template <typename T, int kBlock = kFlatBlock, int kUnroll = kFlatUnroll>
+__global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
+    const T* x, T* g, uint32_t n_vec, uint32_t vpr, int64_t ld, int64_t ldg,
+    const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
+    const float* __restrict__ g_sum, const float* __restrict__ gout, int64_t gstride) {
+  using E = Elem<T>;
+  constexpr int EPV = E::kPerVec;
+  const uint32_t base = blockIdx.x * static_cast<uint32_t>(kBlock * kUnroll) + threadIdx.x;
+  u32x4 v[kUnroll];
+  uint32_t rows[kUnroll], cols[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t f = base + u * kBlock;
+    rows[u] = f / vpr;
+    cols[u] = (f - rows[u] * vpr) * EPV;
+    if (f < n_vec)
+      v[u] = load_stream(reinterpret_cast<const u32x4*>(x + rows[u] * ld + cols[u]));
+  }
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) {
+    const uint32_t f = base + u * kBlock;
+    if (f >= n_vec) continue;
+    const uint32_t row = rows[u];
+    const float M = g_max[row];
+    const float S = g_sum[row];
+    const float go = gout[row * gstride];
+    const float mc = M * kLog2e;
+    const float scale = go / S;
+    const int64_t d = target[row] - vstart - cols[u];
+    float f32[EPV], y[EPV];
+    E::unpack(v[u], f32);
+#pragma unroll
+    for (int k = 0; k < EPV; ++k) y[k] = exp2_hw(fmaf(f32[k], kLog2e, -mc)) * scale;
+    if (static_cast<uint64_t>(d) < static_cast<uint64_t>(EPV)) {
+#pragma unroll
+      for (int k = 0; k < EPV; ++k)
+        if (k == d) y[k] = target_grad(f32[k], mc, S, go);
+    }
+    store_stream(reinterpret_cast<u32x4*>(g + row * ldg + cols[u]), E::pack(y));
+  }
+}
+
 inline unsigned grid_for_rows(int64_t n_rows) {
   const int64_t cap = int64_t(1) << 30;
   return static_cast<unsigned>(n_rows < cap ? n_rows : cap);
@@ -264,6 +338,38 @@ inline int launch_status() {
 }  // namespace nmce
 
 using namespace nmce;
+
+namespace {
+int check_fwd_args(const void* logits, int dtype, int64_t n_rows, int64_t vocab_local, int64_t ld,
+                   const int64_t* target, const float* o0, const float* o1, const float* o2) {
+  if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
+  if (n_rows < 0 || vocab_local < 1 || ld < vocab_local) return NMCE_EINVAL_SHAPE;
+  if (n_rows == 0) return NMCE_OK;
+  if (!logits || !target || !o0 || !o1 || !o2) return NMCE_EINVAL_PTR;
+  const size_t es = dtype == NMCE_F32 ? 4 : 2;
+  if (reinterpret_cast<uintptr_t>(logits) % es) return NMCE_EINVAL_ALIGN;
+  return NMCE_OK;
+}
+
+template <bool kFinal>
+int launch_stats(const void* logits, int dtype, int64_t n_rows, int64_t vocab_local, int64_t ld,
+                 const int64_t* target, int64_t vocab_start, float* o0, float* o1, float* o2,
+                 void* stream) {
+  const int rc = check_fwd_args(logits, dtype, n_rows, vocab_local, ld, target, o0, o1, o2);
+  if (rc != NMCE_OK || n_rows == 0) return rc;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(grid_for_rows(n_rows)), block(kStatsBlock);
+  if (dtype == NMCE_F32)
+    hipLaunchKernelGGL((ce_stats_kernel<float, kFinal>), grid, block, 0, st,
+                       static_cast<const float*>(logits), n_rows, vocab_local, ld, target,
+                       vocab_start, o0, o1, o2);
+  else
+    hipLaunchKernelGGL((ce_stats_kernel<uint16_t, kFinal>), grid, block, 0, st,
+                       static_cast<const uint16_t*>(logits), n_rows, vocab_local, ld, target,
+                       vocab_start, o0, o1, o2);
+  return launch_status();
+}
+}  // namespace
 
 extern "C" {
 
@@ -286,23 +392,15 @@ int nmce_version(void) { return (1 << 16) | 0; }
 int nmce_ce_fwd_stats(const void* logits, int dtype, int64_t n_rows, int64_t vocab_local,
                       int64_t ld, const int64_t* target, int64_t vocab_start, float* row_max,
                       float* row_sumexp, float* target_logit, void* stream) {
-  if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
-  if (n_rows < 0 || vocab_local < 1 || ld < vocab_local) return NMCE_EINVAL_SHAPE;
-  if (n_rows == 0) return NMCE_OK;
-  if (!logits || !target || !row_max || !row_sumexp || !target_logit) return NMCE_EINVAL_PTR;
-  const size_t es = dtype == NMCE_F32 ? 4 : 2;
-  if (reinterpret_cast<uintptr_t>(logits) % es) return NMCE_EINVAL_ALIGN;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(grid_for_rows(n_rows)), block(kBlock);
-  if (dtype == NMCE_F32)
-    hipLaunchKernelGGL(ce_stats_kernel<float>, grid, block, 0, st,
-                       static_cast<const float*>(logits), n_rows, vocab_local, ld, target,
-                       vocab_start, row_max, row_sumexp, target_logit);
-  else
-    hipLaunchKernelGGL(ce_stats_kernel<uint16_t>, grid, block, 0, st,
-                       static_cast<const uint16_t*>(logits), n_rows, vocab_local, ld, target,
-                       vocab_start, row_max, row_sumexp, target_logit);
-  return launch_status();
+  return launch_stats<false>(logits, dtype, n_rows, vocab_local, ld, target, vocab_start,
+                             row_max, row_sumexp, target_logit, stream);
+}
+
+int nmce_ce_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t ld,
+                const int64_t* target, float* loss, float* g_max, float* g_sumexp,
+                void* stream) {
+  return launch_stats<true>(logits, dtype, n_rows, vocab, ld, target, 0, g_max, g_sumexp, loss,
+                            stream);
 }
 
 int nmce_ce_combine(const float* row_max, const float* row_sumexp, const float* target_logit,
@@ -354,7 +452,30 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64
   // from a 16-byte boundary.
   const bool vec = ((px - pg) % 16 == 0) && (((ld - ld_grad) * static_cast<int64_t>(es)) % 16 == 0);
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(grid_for_rows(n_rows)), block(kBlock);
+  // Flat path: every row of both tensors starts on a 16-byte boundary and
+  // holds a whole number of vectors.
+  const int64_t epv = 16 / static_cast<int64_t>(es);
+  const int64_t vpr = vocab_local / epv;
+  const bool flat = px % 16 == 0 && pg % 16 == 0 && (ld * static_cast<int64_t>(es)) % 16 == 0 &&
+                    (ld_grad * static_cast<int64_t>(es)) % 16 == 0 && vocab_local % epv == 0 &&
+                    n_rows * vpr < (int64_t(1) << 31);
+  if (flat) {
+    const int64_t n_vec = n_rows * vpr;
+    const int64_t per_block = kFlatBlock * kFlatUnroll;
+    const dim3 fgrid(static_cast<unsigned>((n_vec + per_block - 1) / per_block));
+    if (dtype == NMCE_F32)
+      hipLaunchKernelGGL((ce_bwd_flat_kernel<float>), fgrid, dim3(kFlatBlock), 0, st,
+                         static_cast<const float*>(logits), static_cast<float*>(grad),
+                         static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
+                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride);
+    else
+      hipLaunchKernelGGL((ce_bwd_flat_kernel<uint16_t>), fgrid, dim3(kFlatBlock), 0, st,
+                         static_cast<const uint16_t*>(logits), static_cast<uint16_t*>(grad),
+                         static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
+                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride);
+    return launch_status();
+  }
+  const dim3 grid(grid_for_rows(n_rows)), block(kBwdBlock);
 #define NMCE_BWD_LAUNCH(T, V)                                                              \
   hipLaunchKernelGGL((ce_bwd_kernel<T, V>), grid, block, 0, st, static_cast<const T*>(logits), \
                      static_cast<T*>(grad), n_rows, vocab_local, ld, ld_grad, target,           \

@@ -20,7 +20,7 @@ LIB_PATH = pathlib.Path(__file__).resolve().parent / "libnmce.so"
 
 NMCE_F32 = 0
 NMCE_BF16 = 1
-NMCE_VALIDATE_ROWS_PER_SLOT = 4096
+NMCE_VALIDATE_ROWS_PER_SLOT = 1024
 
 _c_int = ctypes.c_int
 _i64 = ctypes.c_int64
@@ -31,6 +31,7 @@ SIGNATURES: dict[str, tuple] = {
     "nmce_status_string": (ctypes.c_char_p, [_c_int]),
     "nmce_version": (_c_int, []),
     "nmce_ce_fwd_stats": (_c_int, [_p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _p]),
+    "nmce_ce_fwd": (_c_int, [_p, _c_int, _i64, _i64, _i64, _p, _p, _p, _p, _p]),
     "nmce_ce_combine": (_c_int, [_p, _p, _p, _c_int, _i64, _i64, _p, _p, _p, _p]),
     "nmce_validate_slots": (_i64, [_i64]),
     "nmce_validate_targets": (_c_int, [_p, _i64, _i64, _p, _p]),

@@ -85,12 +85,26 @@ def _check_inputs(logits: torch.Tensor, target: torch.Tensor, vocab_start: int,
             f"[{vocab_start}, {vocab_end}) has {vocab_end - vocab_start}")
 
 
-def validate_targets(target: torch.Tensor, vocab_size: int) -> None:
-    """Raise ``ValueError`` if any target is outside ``[0, vocab_size)``.
+class _PendingCheck:
+    """Bad-target counts on their way to pinned host memory."""
 
-    Same check and message as cross_entropy.py:79-81, run as one kernel and
-    one small device-to-host read (the reference uses two ``torch.any``
-    reductions, each a host sync).
+    def __init__(self, host: torch.Tensor, event: torch.cuda.Event):
+        self.host = host
+        self.event = event
+
+    def raise_if_bad(self) -> None:
+        self.event.synchronize()
+        if int(self.host.sum()) != 0:
+            raise ValueError("target token id is outside the model vocabulary")
+
+
+def launch_target_check(target: torch.Tensor, vocab_size: int) -> _PendingCheck | None:
+    """Start the target check of cross_entropy.py:79-81 without blocking.
+
+    One kernel counts targets outside ``[0, vocab_size)`` and the counts are
+    copied into pinned host memory; ``raise_if_bad()`` on the result waits
+    for that copy alone. Enqueue the loss kernels before waiting, so the GPU
+    keeps working while the host checks.
     """
     lib = _lib.load()
     t = target.reshape(-1)
@@ -98,13 +112,28 @@ def validate_targets(target: torch.Tensor, vocab_size: int) -> None:
         t = t.contiguous()
     n = t.numel()
     if n == 0:
-        return
+        return None
     slots = lib.nmce_validate_slots(n)
     counts = torch.empty(slots, dtype=torch.int32, device=t.device)
     _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n, vocab_size,
             counts.data_ptr(), _lib.stream_handle(t.device))
-    if int(counts.cpu().sum()) != 0:
-        raise ValueError("target token id is outside the model vocabulary")
+    host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
+    host.copy_(counts, non_blocking=True)
+    event = torch.cuda.Event()
+    event.record()
+    return _PendingCheck(host, event)
+
+
+def validate_targets(target: torch.Tensor, vocab_size: int) -> None:
+    """Raise ``ValueError`` if any target is outside ``[0, vocab_size)``.
+
+    Same check and message as cross_entropy.py:79-81, as one kernel and one
+    small device-to-host read (the reference runs two ``torch.any``
+    reductions, each a host sync).
+    """
+    pending = launch_target_check(target, vocab_size)
+    if pending is not None:
+        pending.raise_if_bad()
 
 
 def _exchange_stats(local: torch.Tensor, group, world_size: int) -> torch.Tensor:
@@ -150,20 +179,24 @@ class _VocabParallelCrossEntropy(torch.autograd.Function):
         if not tgt.is_contiguous():
             tgt = tgt.contiguous()
 
-        local = torch.empty((3, n), dtype=torch.float32, device=dev)
-        _launch("nmce_ce_fwd_stats", lib.nmce_ce_fwd_stats,
-                rows.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ld, tgt.data_ptr(),
-                vocab_start, local[0].data_ptr(), local[1].data_ptr(), local[2].data_ptr(), stream)
-
-        if world_size > 1:
-            stats = _exchange_stats(local, group, world_size)
+        dcode = _lib.dtype_code(rows.dtype)
+        # out[0] = per-token loss, out[1] = global row max, out[2] = global exp-sum
+        out = torch.empty((3, n), dtype=torch.float32, device=dev)
+        loss, row_stat = out[0], out[1:]
+        if world_size == 1:
+            # One shard holds the whole vocabulary: statistics and loss in one pass.
+            _launch("nmce_ce_fwd", lib.nmce_ce_fwd, rows.data_ptr(), dcode, n, V, ld,
+                    tgt.data_ptr(), loss.data_ptr(), row_stat[0].data_ptr(),
+                    row_stat[1].data_ptr(), stream)
         else:
-            stats = local
-        loss = torch.empty(n, dtype=torch.float32, device=dev)
-        row_stat = torch.empty((2, n), dtype=torch.float32, device=dev)  # global max, exp-sum
-        _launch("nmce_ce_combine", lib.nmce_ce_combine,
-                stats.data_ptr(), stats.data_ptr() + 4 * n, stats.data_ptr() + 8 * n, world_size,
-                3 * n, n, loss.data_ptr(), row_stat[0].data_ptr(), row_stat[1].data_ptr(), stream)
+            local = torch.empty((3, n), dtype=torch.float32, device=dev)
+            _launch("nmce_ce_fwd_stats", lib.nmce_ce_fwd_stats, rows.data_ptr(), dcode, n, V, ld,
+                    tgt.data_ptr(), vocab_start, local[0].data_ptr(), local[1].data_ptr(),
+                    local[2].data_ptr(), stream)
+            stats = _exchange_stats(local, group, world_size)
+            _launch("nmce_ce_combine", lib.nmce_ce_combine, stats.data_ptr(),
+                    stats.data_ptr() + 4 * n, stats.data_ptr() + 8 * n, world_size, 3 * n, n,
+                    loss.data_ptr(), row_stat[0].data_ptr(), row_stat[1].data_ptr(), stream)
 
         ctx.inplace = bool(inplace)
         ctx.vocab_start = vocab_start
@@ -227,8 +260,12 @@ def vocab_parallel_cross_entropy(
     """
     _check_inputs(logits, target, vocab_start, vocab_end)
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
-    if validate:
-        validate_targets(target, vocab_size)
+    pending = launch_target_check(target, vocab_size) if validate else None
+    # The loss kernels are enqueued before the host waits for the check, so
+    # the GPU is busy while the host reads the counts. They never read out of
+    # bounds on a bad target; their result is discarded when the check fails.
     loss = _VocabParallelCrossEntropy.apply(
         logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace)
+    if pending is not None:
+        pending.raise_if_bad()
     return loss.mean()

@@ -50,6 +50,11 @@ def test_argument_errors_before_launch(lib):
     assert lib.nmce_ce_fwd_stats(p, 1, 0, 8, 8, None, 0, None, None, None, None) == 0
     assert lib.nmce_ce_fwd_stats(p, 1, 4, 8, 8, None, 0, p, p, p, None) == -4
     assert lib.nmce_ce_fwd_stats(p + 1, 1, 4, 8, 8, p, 0, p, p, p, None) == -3
+    assert lib.nmce_ce_fwd(p, 3, 4, 8, 8, p, p, p, p, None) == -1
+    assert lib.nmce_ce_fwd(p, 0, 4, 8, 7, p, p, p, p, None) == -2
+    assert lib.nmce_ce_fwd(p, 0, 4, 8, 8, p, None, p, p, None) == -4
+    assert lib.nmce_ce_fwd(p + 2, 0, 4, 8, 8, p, p, p, p, None) == -3
+    assert lib.nmce_ce_fwd(p, 0, 0, 8, 8, None, None, None, None, None) == 0
     assert lib.nmce_ce_combine(p, p, p, 0, 4, 4, p, p, p, None) == -5
     assert lib.nmce_ce_combine(p, p, p, 2, 3, 4, p, p, p, None) == -2
     assert lib.nmce_ce_combine(None, p, p, 1, 4, 4, p, p, p, None) == -4
@@ -64,9 +69,9 @@ def test_argument_errors_before_launch(lib):
 def test_validate_slots(lib):
     assert lib.nmce_validate_slots(0) == 0
     assert lib.nmce_validate_slots(1) == 1
-    assert lib.nmce_validate_slots(4096) == 1
-    assert lib.nmce_validate_slots(4097) == 2
-    assert lib.nmce_validate_slots(16384) == 4
+    assert lib.nmce_validate_slots(1024) == 1
+    assert lib.nmce_validate_slots(1025) == 2
+    assert lib.nmce_validate_slots(16384) == 16
 
 
 def test_dropin_has_no_cpu_path():
