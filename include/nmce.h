@@ -126,6 +126,16 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows,
                 const float* g_sumexp, const float* grad_output,
                 int64_t gout_stride, void* stream);
 
+/*
+ * Measurement support (no counterpart in the reference): a plain copy of
+ * `bytes` (multiple of 16, both pointers 16-byte aligned) with the loss
+ * kernels' access pattern -- 16-byte non-temporal loads and stores. Its HBM
+ * traffic is known exactly, so hardware byte counters (FETCH_SIZE,
+ * WRITE_SIZE) read for it give the scale factors for the same counters read
+ * on the loss kernels.
+ */
+int nmce_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -30,10 +30,10 @@ namespace nmce {
 namespace {
 
 constexpr int kStatsBlock = 1024;
-constexpr int kStatsUnroll = 4;
+constexpr int kStatsUnroll = 2;
 constexpr int kBwdBlock = 1024;   // row-per-workgroup backward
 constexpr int kBwdUnroll = 4;
-constexpr int kFlatBlock = 256;   // flat backward
+constexpr int kFlatBlock = 128;   // flat backward
 constexpr int kFlatUnroll = 2;
 constexpr int kValidateThreads = 256;
 // Running maxima start here instead of -inf so that rows (or lanes) that have
@@ -324,6 +324,23 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
   }
 }
 
+// Plain 16-byte streaming copy with the flat backward's access pattern
+// (non-temporal loads and stores, kFlatBlock x kFlatUnroll vectors per
+// workgroup). Its traffic is known exactly, so hardware byte counters read
+// for it calibrate the counters read for the loss kernels.
+__global__ __launch_bounds__(kFlatBlock) void stream_copy_kernel(const u32x4* __restrict__ src,
+                                                                 u32x4* __restrict__ dst,
+                                                                 int64_t n_vec) {
+  const int64_t base = static_cast<int64_t>(blockIdx.x) * (kFlatBlock * kFlatUnroll) + threadIdx.x;
+  u32x4 v[kFlatUnroll];
+#pragma unroll
+  for (int u = 0; u < kFlatUnroll; ++u)
+    if (base + u * kFlatBlock < n_vec) v[u] = load_stream(src + base + u * kFlatBlock);
+#pragma unroll
+  for (int u = 0; u < kFlatUnroll; ++u)
+    if (base + u * kFlatBlock < n_vec) store_stream(dst + base + u * kFlatBlock, v[u]);
+}
+
 inline unsigned grid_for_rows(int64_t n_rows) {
   const int64_t cap = int64_t(1) << 30;
   return static_cast<unsigned>(n_rows < cap ? n_rows : cap);
@@ -486,6 +503,22 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64
     if (vec) NMCE_BWD_LAUNCH(uint16_t, true); else NMCE_BWD_LAUNCH(uint16_t, false);
   }
 #undef NMCE_BWD_LAUNCH
+  return launch_status();
+}
+
+int nmce_stream_copy(const void* src, void* dst, int64_t bytes, void* stream) {
+  if (bytes < 0 || bytes % 16) return NMCE_EINVAL_SHAPE;
+  if (bytes == 0) return NMCE_OK;
+  if (!src || !dst) return NMCE_EINVAL_PTR;
+  if (reinterpret_cast<uintptr_t>(src) % 16 || reinterpret_cast<uintptr_t>(dst) % 16)
+    return NMCE_EINVAL_ALIGN;
+  const int64_t n_vec = bytes / 16;
+  const int64_t per_block = kFlatBlock * kFlatUnroll;
+  const int64_t blocks = (n_vec + per_block - 1) / per_block;
+  if (blocks > INT32_MAX) return NMCE_EINVAL_SHAPE;
+  hipLaunchKernelGGL(stream_copy_kernel, dim3(static_cast<unsigned>(blocks)), dim3(kFlatBlock), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const u32x4*>(src),
+                     static_cast<u32x4*>(dst), n_vec);
   return launch_status();
 }
 

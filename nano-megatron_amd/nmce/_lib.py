@@ -35,6 +35,7 @@ SIGNATURES: dict[str, tuple] = {
     "nmce_ce_combine": (_c_int, [_p, _p, _p, _c_int, _i64, _i64, _p, _p, _p, _p]),
     "nmce_validate_slots": (_i64, [_i64]),
     "nmce_validate_targets": (_c_int, [_p, _i64, _i64, _p, _p]),
+    "nmce_stream_copy": (_c_int, [_p, _p, _i64, _p]),
     "nmce_ce_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _p]),
 }
 

@@ -98,13 +98,27 @@ class _PendingCheck:
             raise ValueError("target token id is outside the model vocabulary")
 
 
+_side_streams: dict[int, torch.cuda.Stream] = {}
+
+
+def _side_stream(device: torch.device) -> torch.cuda.Stream:
+    """A per-device stream (default priority) for the target check."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    stream = _side_streams.get(idx)
+    if stream is None:
+        stream = torch.cuda.Stream(device=idx)
+        _side_streams[idx] = stream
+    return stream
+
+
 def launch_target_check(target: torch.Tensor, vocab_size: int) -> _PendingCheck | None:
     """Start the target check of cross_entropy.py:79-81 without blocking.
 
     One kernel counts targets outside ``[0, vocab_size)`` and the counts are
-    copied into pinned host memory; ``raise_if_bad()`` on the result waits
-    for that copy alone. Enqueue the loss kernels before waiting, so the GPU
-    keeps working while the host checks.
+    copied into pinned host memory, both on a side stream ordered after the
+    work already queued on the current stream; ``raise_if_bad()`` on the
+    result waits for that copy alone. The loss kernels go on the current
+    stream meanwhile, so the check adds nothing to the loss stream's timeline.
     """
     lib = _lib.load()
     t = target.reshape(-1)
@@ -114,13 +128,18 @@ def launch_target_check(target: torch.Tensor, vocab_size: int) -> _PendingCheck 
     if n == 0:
         return None
     slots = lib.nmce_validate_slots(n)
-    counts = torch.empty(slots, dtype=torch.int32, device=t.device)
-    _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n, vocab_size,
-            counts.data_ptr(), _lib.stream_handle(t.device))
-    host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
-    host.copy_(counts, non_blocking=True)
-    event = torch.cuda.Event()
-    event.record()
+    main = torch.cuda.current_stream(t.device)
+    side = _side_stream(t.device)
+    side.wait_stream(main)  # the targets are complete in the current stream's order
+    with torch.cuda.stream(side):
+        counts = torch.empty(slots, dtype=torch.int32, device=t.device)
+        _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
+                vocab_size, counts.data_ptr(), side.cuda_stream)
+        host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
+        host.copy_(counts, non_blocking=True)
+        event = torch.cuda.Event()
+        event.record(side)
+    t.record_stream(side)  # keep the targets' memory until the side stream is done
     return _PendingCheck(host, event)
 
 

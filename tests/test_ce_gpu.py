@@ -475,3 +475,16 @@ def test_validation_overlaps_and_still_raises_before_returning():
     loss = nmce.vocab_parallel_cross_entropy(x, t, 0, 1000, nmce.ParallelContext.single())
     ref = _torch_ref_rows(x.view(-1, 1000), t.view(-1)).mean()
     assert abs(loss.item() - ref.item()) <= 1e-5 * abs(ref.item())
+
+
+def test_stream_copy_calibration_kernel():
+    """nmce_stream_copy copies exactly (it calibrates the byte counters)."""
+    from nmce import _lib as L
+    lib = L.load()
+    src = torch.randint(-2**31, 2**31 - 1, (4 * 1000 + 4,), dtype=torch.int32, device=DEV)
+    dst = torch.zeros_like(src)
+    L.check(lib.nmce_stream_copy(src.data_ptr(), dst.data_ptr(), src.numel() * 4,
+                                 L.stream_handle(torch.device(DEV))), "copy")
+    torch.cuda.synchronize()
+    assert torch.equal(src, dst)
+    assert lib.nmce_stream_copy(src.data_ptr(), dst.data_ptr(), 12, None) == -2
