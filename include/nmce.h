@@ -136,6 +136,71 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows,
  */
 int nmce_stream_copy(const void* src, void* dst, int64_t bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * Fused LM head + cross entropy (bf16 only).
+ *
+ * Replaces ParallelLMHead.forward's projection logits = hidden @ weight.t()
+ * (model.py:192, bf16 under autocast per model.py:255-257) followed by the
+ * loss of cross_entropy.py:16-65, without storing the [n_rows, vocab_local]
+ * logits. hidden is [n_rows, hidden_size] and weight (the vocabulary shard of
+ * the tied embedding, tp_layers.py:108) is [vocab_local, hidden_size], both
+ * row-major with row stride hidden_size, 16-byte aligned; hidden_size must be
+ * a multiple of 64. Logits are accumulated in fp32 and not rounded to bf16.
+ * --------------------------------------------------------------------------- */
+
+/* Device workspace bytes needed by nmce_lmhead_ce_fwd_stats. */
+int64_t nmce_lmhead_ce_fwd_workspace_bytes(int64_t n_rows, int64_t hidden_size,
+                                           int64_t vocab_local);
+
+/*
+ * Per-shard statistics of the logits hidden @ weight^T, as nmce_ce_fwd_stats
+ * computes them for a stored logit slab (cross_entropy.py:21, :28-36,
+ * :40-41 on the shard [vocab_start, vocab_start + vocab_local)). Combine the
+ * shards with nmce_ce_combine (tp = 1 for a single shard).
+ */
+int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                             int64_t hidden_size, int64_t vocab_local, const int64_t* target,
+                             int64_t vocab_start, float* row_max, float* row_sumexp,
+                             float* target_logit, void* workspace, int64_t workspace_bytes,
+                             void* stream);
+
+/* Device workspace bytes needed by nmce_lmhead_ce_bwd for a vocabulary chunk
+ * of vocab_chunk rows (<= 0: the whole shard in one chunk). */
+int64_t nmce_lmhead_ce_bwd_workspace_bytes(int64_t n_rows, int64_t hidden_size,
+                                           int64_t vocab_local, int64_t vocab_chunk);
+
+/*
+ * Backward of the fused LM head + loss (cross_entropy.py:53-65 followed by
+ * the matmul backward of model.py:192):
+ *   dZ[r, j]        = (exp(z[r, j] - g_max[r]) / g_sumexp[r]
+ *                      - [j == target[r] - vocab_start]) * grad_output[r*gout_stride]
+ *   grad_hidden     = dZ @ weight          [n_rows, hidden_size] bf16
+ *   grad_weight     = dZ^T @ hidden        [vocab_local, hidden_size] bf16
+ * with z = hidden @ weight^T recomputed chunk by chunk (vocab_chunk rows of
+ * the shard at a time) and dZ rounded to bf16 before the two products, as the
+ * reference's autocast matmul backward consumes a bf16 gradient. g_max and
+ * g_sumexp are the combined statistics of the forward (nmce_ce_combine).
+ * grad_hidden is this shard's contribution only (the TP all-reduce of the
+ * input gradient, mappings.py:83-94, belongs to the caller).
+ */
+int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                       int64_t hidden_size, int64_t vocab_local, const int64_t* target,
+                       int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                       const float* grad_output, int64_t gout_stride, void* grad_hidden,
+                       void* grad_weight, int64_t vocab_chunk, void* workspace,
+                       int64_t workspace_bytes, void* stream);
+
+/*
+ * The GEMM core of the fused path, exposed for testing and measurement (no
+ * counterpart in the reference): c[i, j] = sum_l a[i, l] * b[j, l] for
+ * i < m, j < n, l < k, with bf16 a [m, lda] and b [n, ldb], fp32
+ * accumulation, and c [m, ldc] written as c_dtype (NMCE_BF16 or NMCE_F32).
+ * k must be a multiple of 64; a and b 16-byte aligned, lda and ldb multiples
+ * of 8.
+ */
+int nmce_gemm_nt_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t m,
+                      int64_t n, int64_t k, void* c, int c_dtype, int64_t ldc, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

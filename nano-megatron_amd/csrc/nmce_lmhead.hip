@@ -1,0 +1,649 @@
+// Fused LM head + vocabulary-parallel cross entropy for gfx950.
+//
+// Replaces ParallelLMHead's projection Z = X @ W^T (nano_megatron/model.py:192,
+// run in bf16 under autocast, model.py:255-257) followed by the loss of
+// nano_megatron/cross_entropy.py:16-65, without ever holding Z for the whole
+// vocabulary.
+//
+// Every product is one bf16 "NT" GEMM shape, C[m, n] = sum_k A[m, k] * B[n, k]
+// with both operands K-contiguous, on v_mfma_f32_32x32x16_bf16:
+//
+//   forward   Z^T = W X^T    (M = vocab, N = tokens, K = hidden). The epilogue
+//             reduces each 128-row vocabulary block of a token's column to a
+//             partial (max, sum exp, target logit); Z is never stored.
+//   backward  per vocabulary chunk of Vc rows:
+//             dZ^T_c = recompute(W_c X^T) -> (softmax - onehot) * g, written as
+//                      bf16 in both layouts [Vc, tokens] and [tokens, Vc]
+//             dW_c   = dZ^T_c X      (M = Vc, N = hidden, K = tokens; B = X^T)
+//             dX    += dZ_c W_c      (M = tokens, N = hidden, K = Vc; B = W^T)
+//
+// Tokens are the MFMA N dimension in the loss GEMMs: the 32x32 accumulator
+// gives each lane 16 vocabulary rows of a single token, so the per-token
+// reductions are mostly in-register, with one cross-half shuffle.
+//
+// Main loop: a 256x256 output tile per 256-lane workgroup (four waves, 2x2,
+// each 128x128 = 16 accumulators of 32x32), K in steps of 64. Operand tiles
+// move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (global_load_lds_dwordx4,
+// no VGPR staging), double-buffered, rows of 128 bytes with the 16-byte chunks
+// XOR-swizzled by (row & 7) so that the ds_read_b128 fragment reads are free
+// of bank conflicts. Workgroups are mapped to tiles so that each XCD (one L2)
+// owns a contiguous band of tiles walked in groups that share operands.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nmce.h"
+#include "nmce_device.h"
+
+namespace nmce {
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+constexpr int kBM = 256;          // tile rows (GEMM M)
+constexpr int kBN = 256;          // tile columns (GEMM N)
+constexpr int kBK = 64;           // K per stage (128 bytes of bf16 per row)
+constexpr int kWavesM = 2;
+constexpr int kWavesN = 2;
+constexpr int kThreads = 64 * kWavesM * kWavesN;
+constexpr int kWaveM = kBM / kWavesM;  // 128
+constexpr int kWaveN = kBN / kWavesN;  // 128
+constexpr int kFM = kWaveM / 32;       // 4 accumulators down
+constexpr int kFN = kWaveN / 32;       // 4 accumulators across
+constexpr int kStageA = kBM * kBK * 2;  // bytes
+constexpr int kStageB = kBN * kBK * 2;
+constexpr int kStage = kStageA + kStageB;
+constexpr int kLdsBytes = 2 * kStage;  // 128 KiB of the 160 KiB per CU
+// 1 KiB LDS blocks (8 rows x 128 B) per stage and per wave.
+constexpr int kBlocksA = kBM / 8;
+constexpr int kBlocksB = kBN / 8;
+constexpr int kBlocksPerWave = (kBlocksA + kBlocksB) / (kWavesM * kWavesN);
+static_assert(kBlocksA % kBlocksPerWave == 0, "a wave loads blocks of one operand only");
+constexpr int kGroupM = 8;         // tile rows per raster group inside an XCD band
+constexpr int kXcds = 8;
+constexpr float kMaxFloorL = -1.0e38f;
+
+// Partial statistics cover this many vocabulary rows (one wave's rows).
+constexpr int kPartialRows = kWaveM;
+
+struct Acc {
+  f32x16_t c[kFM][kFN];
+};
+
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// Tile index for this workgroup. The dispatcher deals workgroups to the 8 XCDs
+// round-robin (block b runs on XCD b % 8); give each XCD a contiguous band of
+// tile ids, and inside the band walk groups of kGroupM tile rows column by
+// column, so the tiles that run together on one L2 share A and B stripes.
+__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int total = tiles_m * tiles_n;
+  const int b = blockIdx.x;
+  const int xcd = b % kXcds;
+  const int q = total / kXcds, r = total % kXcds;
+  const int tid = xcd * q + (xcd < r ? xcd : r) + b / kXcds;
+  const int group = kGroupM * tiles_n;
+  const int g = tid / group;
+  const int first_m = g * kGroupM;
+  const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  const int in_g = tid - g * group;
+  tm = first_m + in_g % gm;
+  tn = in_g / gm;
+}
+
+// The main loop: acc = A[m0:m0+256, 0:K] * B[n0:n0+256, 0:K]^T.
+// A rows >= M and B rows >= N are read from the last valid row (their results
+// are masked by the epilogues). Requires K % 64 == 0, lda and ldb multiples of
+// 8 elements, 16-byte aligned A and B, and 256*ld*2 < 2^32 bytes.
+__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t lda,
+                                              int64_t M, const uint16_t* __restrict__ B,
+                                              int64_t ldb, int64_t N, int64_t K, int64_t m0,
+                                              int64_t n0, char* lds, Acc& acc) {
+  const int lane = threadIdx.x & 63;
+  // The wave index is uniform across the wave; say so, so that the load
+  // bases and LDS destinations below live in scalar registers.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+
+#pragma unroll
+  for (int i = 0; i < kFM; ++i)
+#pragma unroll
+    for (int j = 0; j < kFN; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc.c[i][j][e] = 0.0f;
+
+  // ---- load plan: this wave fills kBlocksPerWave 1 KiB blocks per stage ----
+  // Lane p of a block writes LDS bytes [16p, 16p+16): row p/8 of the block,
+  // physical chunk p%8, which holds logical chunk (p%8) ^ (row & 7).
+  const int first_block = wave * kBlocksPerWave;
+  const bool load_a = first_block < kBlocksA;
+  const int row_lane = lane >> 3;
+  const int chunk = (lane & 7) ^ row_lane;
+  const char* gbase;
+  int64_t ld_op, rows_op;
+  int lds_op;
+  int blk0;
+  if (load_a) {
+    gbase = reinterpret_cast<const char*>(A + m0 * lda);
+    ld_op = lda; rows_op = M - m0; lds_op = 0; blk0 = first_block;
+  } else {
+    gbase = reinterpret_cast<const char*>(B + n0 * ldb);
+    ld_op = ldb; rows_op = N - n0; lds_op = kStageA; blk0 = first_block - kBlocksA;
+  }
+  uint32_t goff[kBlocksPerWave];
+#pragma unroll
+  for (int j = 0; j < kBlocksPerWave; ++j) {
+    int64_t r = (blk0 + j) * 8 + row_lane;
+    if (r > rows_op - 1) r = rows_op - 1;
+    goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
+  }
+
+  auto issue = [&](int stage, int64_t k0) {
+    const char* g = gbase + k0 * 2;
+    char* l = lds + stage * kStage + lds_op + blk0 * 1024;
+#pragma unroll
+    for (int j = 0; j < kBlocksPerWave; ++j) {
+      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + goff[j]),
+                                       (lds_void_t*)(l + j * 1024), 16, 0, 0);
+    }
+  };
+
+  // ---- fragment plan: 32x32x16 operands, 8 bf16 per lane -------------------
+  // A fragment fm, K sub-step s: row wm*128 + 32*fm + lane%32, logical chunk
+  // 2*s + lane/32 of that row (16 bytes).
+  const int frow = lane & 31;
+  const int fhalf = lane >> 5;
+  const int a_row_off = (wm * kWaveM + frow) * 128;
+  const int b_row_off = kStageA + (wn * kWaveN + frow) * 128;
+  int xo[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) xo[s] = (((2 * s + fhalf) ^ (frow & 7)) << 4);
+
+  const int64_t kt_n = K / kBK;
+  issue(0, 0);
+  wait_vmem();
+  __syncthreads();
+  for (int64_t kt = 0; kt < kt_n; ++kt) {
+    const int cur = static_cast<int>(kt & 1);
+    if (kt + 1 < kt_n) issue(cur ^ 1, (kt + 1) * kBK);
+    const char* st = lds + cur * kStage;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8_t a[kFM], b[kFN];
+#pragma unroll
+      for (int i = 0; i < kFM; ++i)
+        a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
+#pragma unroll
+      for (int j = 0; j < kFN; ++j)
+        b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
+#pragma unroll
+      for (int i = 0; i < kFM; ++i)
+#pragma unroll
+        for (int j = 0; j < kFN; ++j)
+          acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc.c[i][j], 0, 0, 0);
+    }
+    wait_vmem();
+    __syncthreads();
+  }
+}
+
+// Row (within the wave's 128 rows) of accumulator fm, element e, for this lane:
+// the 32x32 result gives lane l column l%32 and rows 8*(e/4) + 4*(l/32) + e%4.
+__device__ __forceinline__ int acc_row(int fm, int e, int fhalf) {
+  return 32 * fm + 8 * (e >> 2) + 4 * fhalf + (e & 3);
+}
+
+// ---------------------------------------------------------------------------
+// Forward: Z^T tile -> per (128-row vocabulary block, token) partial stats.
+//   pmax[b*N + t], psum[b*N + t] = max and sum exp(z - max) over the block's
+//   valid rows; ptgt[b*N + t] = z of the target row if it lies in the block,
+//   else 0. (cross_entropy.py:21, :28-36, :40-41 restricted to the block.)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ X, int64_t V, int64_t N,
+    int64_t H, const int64_t* __restrict__ target, int64_t vstart, float* __restrict__ pmax,
+    float* __restrict__ psum, float* __restrict__ ptgt) {
+  extern __shared__ __align__(16) char lds[];
+  const int tiles_m = static_cast<int>((V + kBM - 1) / kBM);
+  const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
+  Acc acc;
+  gemm_mainloop(W, H, V, X, H, N, H, m0, n0, lds, acc);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int fhalf = lane >> 5;
+  const int64_t vrow0 = m0 + wm * kWaveM;  // first vocabulary row of this wave
+  if (vrow0 >= V) return;
+  const int64_t blk = vrow0 / kPartialRows;
+  const int64_t valid_rows = V - vrow0;  // rows >= this are padding
+#pragma unroll
+  for (int fn = 0; fn < kFN; ++fn) {
+    const int64_t tok = n0 + wn * kWaveN + 32 * fn + (lane & 31);
+    const bool tok_ok = tok < N;
+    int64_t tl = -1;
+    if (tok_ok) tl = target[tok] - vstart - vrow0;
+    float mx = kMaxFloorL;
+    float pick = 0.0f;
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = acc_row(fm, e, fhalf);
+        const float z = acc.c[fm][fn][e];
+        if (r < valid_rows) mx = fmaxf(mx, z);
+        pick = (r == tl) ? z : pick;
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mc = mx * kLog2e;
+    float s = 0.0f;
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = acc_row(fm, e, fhalf);
+        const float p = exp2_hw(fmaf(acc.c[fm][fn][e], kLog2e, -mc));
+        s += (r < valid_rows) ? p : 0.0f;
+      }
+    s += __shfl_xor(s, 32);
+    pick += __shfl_xor(pick, 32);
+    if (fhalf == 0 && tok_ok) {
+      pmax[blk * N + tok] = mx;
+      psum[blk * N + tok] = s;
+      ptgt[blk * N + tok] = pick;
+    }
+  }
+}
+
+// Merge the partial statistics of nb vocabulary blocks into shard statistics:
+// max, sum exp relative to it, and the target logit (0 when not in the shard).
+__global__ __launch_bounds__(256) void lmhead_reduce_partials_kernel(
+    const float* __restrict__ pmax, const float* __restrict__ psum,
+    const float* __restrict__ ptgt, int64_t nb, int64_t N, float* __restrict__ row_max,
+    float* __restrict__ row_sumexp, float* __restrict__ target_logit) {
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (t >= N) return;
+  float m = kMaxFloorL;
+  for (int64_t b = 0; b < nb; ++b) m = fmaxf(m, pmax[b * N + t]);
+  const float mc = m * kLog2e;
+  float s = 0.0f, tg = 0.0f;
+  for (int64_t b = 0; b < nb; ++b) {
+    s = fmaf(psum[b * N + t], exp2_hw(fmaf(pmax[b * N + t], kLog2e, -mc)), s);
+    tg += ptgt[b * N + t];
+  }
+  row_max[t] = m;
+  row_sumexp[t] = s;
+  target_logit[t] = tg;
+}
+
+// ---------------------------------------------------------------------------
+// Backward, step 1: recompute a chunk of Z^T and write
+//   dZ[v, t] = (exp(z - gmax[t]) / gsum[t] - [v == target[t]]) * g[t]
+// (cross_entropy.py:53-65) as bf16 into dzt[v * ldt + t] and dz[t * ldz + v].
+// Rows v >= Mvalid and tokens t >= N are written as 0 (they pad the K extents
+// of the two GEMMs that follow).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
+    const uint16_t* __restrict__ Wc, const uint16_t* __restrict__ X, int64_t Mvalid,
+    int64_t Mpad, int64_t N, int64_t H, const int64_t* __restrict__ target, int64_t vfirst,
+    const float* __restrict__ gmax, const float* __restrict__ gsum,
+    const float* __restrict__ gout, int64_t gout_stride, uint16_t* __restrict__ dzt,
+    int64_t ldt, uint16_t* __restrict__ dz, int64_t ldz) {
+  extern __shared__ __align__(16) char lds[];
+  const int tiles_m = static_cast<int>(Mpad / kBM);
+  const int tiles_n = static_cast<int>((ldt + kBN - 1) / kBN);
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
+  Acc acc;
+  gemm_mainloop(Wc, H, Mvalid, X, H, N, H, m0, n0, lds, acc);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int fhalf = lane >> 5;
+  const int64_t vrow0 = m0 + wm * kWaveM;
+  const int64_t valid_rows = Mvalid - vrow0;
+#pragma unroll
+  for (int fn = 0; fn < kFN; ++fn) {
+    const int64_t tok = n0 + wn * kWaveN + 32 * fn + (lane & 31);
+    const bool tok_ok = tok < N;
+    float mc = 0.0f, scale = 0.0f, g = 0.0f;
+    int64_t tl = -1;
+    if (tok_ok) {
+      g = gout[tok * gout_stride];
+      mc = gmax[tok] * kLog2e;
+      scale = g / gsum[tok];
+      tl = target[tok] - vfirst - vrow0;
+    }
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm) {
+      float d[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = acc_row(fm, e, fhalf);
+        float p = exp2_hw(fmaf(acc.c[fm][fn][e], kLog2e, -mc)) * scale;
+        p -= (r == tl) ? g : 0.0f;
+        d[e] = (tok_ok && r < valid_rows) ? p : 0.0f;
+      }
+      // dz: 4 consecutive vocabulary rows per group of 4 elements -> 8 bytes.
+      if (tok_ok) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int64_t v = vrow0 + 32 * fm + 8 * q + 4 * fhalf;
+          if (v < Mpad) {
+            uint2 w;
+            w.x = pack_bf16x2(d[4 * q], d[4 * q + 1]);
+            w.y = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
+            *reinterpret_cast<uint2*>(dz + tok * ldz + v) = w;
+          }
+        }
+      }
+      if (tok < ldt) {
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int64_t v = vrow0 + acc_row(fm, e, fhalf);
+          if (v < Mpad) dzt[v * ldt + tok] = f32_to_bf16(d[e]);
+        }
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Plain GEMM with a stored result: C[m, n] (ldc) for m < M, n < N.
+//   kMode 0: C = acc as bf16
+//   kMode 1: Cf = acc (fp32)
+//   kMode 2: Cf += acc (fp32)
+//   kMode 3: C = bf16(Cf + acc)
+// ---------------------------------------------------------------------------
+template <int kMode>
+__global__ __launch_bounds__(kThreads) void gemm_store_kernel(
+    const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
+    int64_t ldb, int64_t N, int64_t K, uint16_t* __restrict__ C, float* __restrict__ Cf,
+    int64_t ldc) {
+  extern __shared__ __align__(16) char lds[];
+  const int tiles_m = static_cast<int>((M + kBM - 1) / kBM);
+  const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
+  int tm, tn;
+  tile_coords(tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
+  Acc acc;
+  gemm_mainloop(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int fhalf = lane >> 5;
+#pragma unroll
+  for (int fn = 0; fn < kFN; ++fn) {
+    const int64_t col = n0 + wn * kWaveN + 32 * fn + (lane & 31);
+    if (col >= N) continue;
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int64_t row = m0 + wm * kWaveM + acc_row(fm, e, fhalf);
+        if (row >= M) continue;
+        const int64_t o = row * ldc + col;
+        const float v = acc.c[fm][fn][e];
+        if constexpr (kMode == 0) C[o] = f32_to_bf16(v);
+        if constexpr (kMode == 1) Cf[o] = v;
+        if constexpr (kMode == 2) Cf[o] += v;
+        if constexpr (kMode == 3) C[o] = f32_to_bf16(Cf[o] + v);
+      }
+  }
+}
+
+// bf16 transpose with zero padding: out[c * ldo + r] = in[r * ldi + c] for
+// r < R, c < C; out[c * ldo + r] = 0 for R <= r < ldo. 64x64 tiles via LDS.
+__global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ in,
+                                                             int64_t R, int64_t C, int64_t ldi,
+                                                             uint16_t* __restrict__ out,
+                                                             int64_t ldo) {
+  __shared__ uint16_t t[64][65];
+  const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64;  // over ldo (padded R)
+  const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t r = r0 + i, c = c0 + tx;
+    t[i][tx] = (r < R && c < C) ? in[r * ldi + c] : static_cast<uint16_t>(0);
+  }
+  __syncthreads();
+  for (int i = ty; i < 64; i += 4) {
+    const int64_t c = c0 + i, r = r0 + tx;
+    if (c < C && r < ldo) out[c * ldo + r] = t[tx][i];
+  }
+}
+
+inline int launch_status() {
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NMCE_OK : static_cast<int>(e);
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+bool lds_configured = false;
+
+int configure_lds() {
+  if (lds_configured) return NMCE_OK;
+  const void* kernels[] = {
+      reinterpret_cast<const void*>(&lmhead_stats_kernel),
+      reinterpret_cast<const void*>(&lmhead_dz_kernel),
+      reinterpret_cast<const void*>(&gemm_store_kernel<0>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<1>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<2>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<3>),
+  };
+  for (const void* k : kernels) {
+    const hipError_t e =
+        hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e != hipSuccess) return static_cast<int>(e);
+  }
+  lds_configured = true;
+  return NMCE_OK;
+}
+
+// A GEMM operand is usable when its base is 16-byte aligned, its row stride is
+// a whole number of 16-byte chunks, and one 256-row tile spans < 4 GiB.
+inline bool operand_ok(const void* p, int64_t ld) {
+  return p != nullptr && aligned16(p) && ld % 8 == 0 && ld > 0 && ld < (int64_t{1} << 22);
+}
+
+int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const uint16_t* B,
+                      int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf, int64_t ldc,
+                      hipStream_t stream) {
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+  const dim3 grid(static_cast<unsigned>(tiles));
+  switch (mode) {
+    case 0: hipLaunchKernelGGL(gemm_store_kernel<0>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
+    case 1: hipLaunchKernelGGL(gemm_store_kernel<1>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
+    case 2: hipLaunchKernelGGL(gemm_store_kernel<2>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
+    default: hipLaunchKernelGGL(gemm_store_kernel<3>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
+  }
+  return launch_status();
+}
+
+int launch_transpose(const uint16_t* in, int64_t R, int64_t C, int64_t ldi, uint16_t* out,
+                     int64_t ldo, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((ldo + 63) / 64));
+  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, stream, in, R, C, ldi, out, ldo);
+  return launch_status();
+}
+
+// Workspace carve-up of the backward (all offsets 256-byte aligned).
+struct BwdLayout {
+  int64_t ldt;    // tokens padded to 64 (K of the dW GEMM)
+  int64_t vpad;   // vocabulary padded to 256 (columns of W^T)
+  int64_t chunk;  // vocabulary rows per chunk (multiple of 256)
+  int64_t n_chunks;
+  int64_t off_xt, off_wt, off_dzt, off_dz, off_acc, total;
+};
+
+inline int64_t align256(int64_t x) { return round_up(x, 256); }
+
+BwdLayout bwd_layout(int64_t n, int64_t h, int64_t v, int64_t chunk) {
+  BwdLayout L{};
+  L.ldt = round_up(n, 64);
+  L.vpad = round_up(v, kBM);
+  L.chunk = chunk <= 0 ? L.vpad : round_up(chunk, kBM);
+  if (L.chunk > L.vpad) L.chunk = L.vpad;
+  L.n_chunks = (L.vpad + L.chunk - 1) / L.chunk;
+  int64_t off = 0;
+  L.off_xt = off; off += align256(h * L.ldt * 2);
+  L.off_wt = off; off += align256(h * L.vpad * 2);
+  L.off_dzt = off; off += align256(L.chunk * L.ldt * 2);
+  L.off_dz = off; off += align256(n * L.chunk * 2);
+  L.off_acc = off; off += L.n_chunks > 1 ? align256(n * h * 4) : 0;
+  L.total = off;
+  return L;
+}
+
+int64_t fwd_partial_blocks(int64_t v) { return (v + kPartialRows - 1) / kPartialRows; }
+
+}  // namespace
+}  // namespace nmce
+
+using namespace nmce;
+
+extern "C" {
+
+int64_t nmce_lmhead_ce_fwd_workspace_bytes(int64_t n_rows, int64_t hidden, int64_t vocab_local) {
+  (void)hidden;
+  if (n_rows < 0 || vocab_local < 0) return -1;
+  return align256(3 * fwd_partial_blocks(vocab_local) * n_rows * 4);
+}
+
+int64_t nmce_lmhead_ce_bwd_workspace_bytes(int64_t n_rows, int64_t hidden, int64_t vocab_local,
+                                           int64_t vocab_chunk) {
+  if (n_rows < 0 || hidden < 0 || vocab_local < 0) return -1;
+  return bwd_layout(n_rows, hidden, vocab_local, vocab_chunk).total;
+}
+
+int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                             int64_t hidden_size, int64_t vocab_local, const int64_t* target,
+                             int64_t vocab_start, float* row_max, float* row_sumexp,
+                             float* target_logit, void* workspace, int64_t workspace_bytes,
+                             void* stream) {
+  if (dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
+  if (n_rows < 0 || vocab_local < 1 || hidden_size < kBK || hidden_size % kBK != 0)
+    return NMCE_EINVAL_SHAPE;
+  if (n_rows == 0) return NMCE_OK;
+  if (!operand_ok(hidden, hidden_size) || !operand_ok(weight, hidden_size))
+    return NMCE_EINVAL_ALIGN;
+  if (!target || !row_max || !row_sumexp || !target_logit) return NMCE_EINVAL_PTR;
+  if (n_rows > (int64_t{1} << 30) || vocab_local > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
+  const int64_t need = nmce_lmhead_ce_fwd_workspace_bytes(n_rows, hidden_size, vocab_local);
+  if (!workspace || workspace_bytes < need || !aligned16(workspace)) return NMCE_EINVAL_WORKSPACE;
+  int st = configure_lds();
+  if (st) return st;
+  auto s = static_cast<hipStream_t>(stream);
+  const int64_t nb = fwd_partial_blocks(vocab_local);
+  float* pmax = static_cast<float*>(workspace);
+  float* psum = pmax + nb * n_rows;
+  float* ptgt = psum + nb * n_rows;
+  const int64_t tiles = ((vocab_local + kBM - 1) / kBM) * ((n_rows + kBN - 1) / kBN);
+  hipLaunchKernelGGL(lmhead_stats_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
+                     kLdsBytes, s, static_cast<const uint16_t*>(weight),
+                     static_cast<const uint16_t*>(hidden), vocab_local, n_rows, hidden_size,
+                     target, vocab_start, pmax, psum, ptgt);
+  if ((st = launch_status())) return st;
+  hipLaunchKernelGGL(lmhead_reduce_partials_kernel,
+                     dim3(static_cast<unsigned>((n_rows + 255) / 256)), dim3(256), 0, s, pmax,
+                     psum, ptgt, nb, n_rows, row_max, row_sumexp, target_logit);
+  return launch_status();
+}
+
+int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                       int64_t hidden_size, int64_t vocab_local, const int64_t* target,
+                       int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                       const float* grad_output, int64_t gout_stride, void* grad_hidden,
+                       void* grad_weight, int64_t vocab_chunk, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  if (dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
+  if (n_rows < 0 || vocab_local < 1 || hidden_size < kBK || hidden_size % kBK != 0)
+    return NMCE_EINVAL_SHAPE;
+  if (n_rows == 0) return NMCE_OK;
+  if (!operand_ok(hidden, hidden_size) || !operand_ok(weight, hidden_size))
+    return NMCE_EINVAL_ALIGN;
+  if (!target || !g_max || !g_sumexp || !grad_output || !grad_hidden || !grad_weight)
+    return NMCE_EINVAL_PTR;
+  if (gout_stride < 0) return NMCE_EINVAL_SHAPE;
+  if (n_rows > (int64_t{1} << 30) || vocab_local > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
+  const BwdLayout L = bwd_layout(n_rows, hidden_size, vocab_local, vocab_chunk);
+  if (L.ldt >= (int64_t{1} << 22) || L.vpad >= (int64_t{1} << 22) || L.chunk >= (int64_t{1} << 22))
+    return NMCE_EINVAL_SHAPE;
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+    return NMCE_EINVAL_WORKSPACE;
+  int st = configure_lds();
+  if (st) return st;
+  auto s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  uint16_t* xt = reinterpret_cast<uint16_t*>(ws + L.off_xt);
+  uint16_t* wt = reinterpret_cast<uint16_t*>(ws + L.off_wt);
+  uint16_t* dzt = reinterpret_cast<uint16_t*>(ws + L.off_dzt);
+  uint16_t* dz = reinterpret_cast<uint16_t*>(ws + L.off_dz);
+  float* acc = reinterpret_cast<float*>(ws + L.off_acc);
+  const auto* X = static_cast<const uint16_t*>(hidden);
+  const auto* W = static_cast<const uint16_t*>(weight);
+  auto* dX = static_cast<uint16_t*>(grad_hidden);
+  auto* dW = static_cast<uint16_t*>(grad_weight);
+  const int64_t H = hidden_size;
+
+  // X^T [H, ldt] and W^T [H, vpad], zero-padded along the token / vocab axis.
+  if ((st = launch_transpose(X, n_rows, H, H, xt, L.ldt, s))) return st;
+  if ((st = launch_transpose(W, vocab_local, H, H, wt, L.vpad, s))) return st;
+
+  for (int64_t c = 0; c < L.n_chunks; ++c) {
+    const int64_t v0 = c * L.chunk;
+    const int64_t mvalid = (vocab_local - v0) < L.chunk ? (vocab_local - v0) : L.chunk;
+    const int64_t mpad = round_up(mvalid, kBM);
+    // dZ of this chunk, both layouts.
+    const int64_t tiles = (mpad / kBM) * ((L.ldt + kBN - 1) / kBN);
+    hipLaunchKernelGGL(lmhead_dz_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
+                       kLdsBytes, s, W + v0 * H, X, mvalid, mpad, n_rows, H, target,
+                       vocab_start + v0, g_max, g_sumexp, grad_output, gout_stride, dzt, L.ldt,
+                       dz, L.chunk);
+    if ((st = launch_status())) return st;
+    // dW rows [v0, v0 + mvalid) = dZ^T_c X  (K = tokens, padded with zeros).
+    if ((st = launch_gemm_store(0, dzt, L.ldt, mvalid, xt, L.ldt, H, L.ldt, dW + v0 * H, nullptr,
+                                H, s)))
+      return st;
+    // dX (+)= dZ_c W_c  (K = the chunk's padded vocabulary rows).
+    int mode;
+    if (L.n_chunks == 1) mode = 0;
+    else if (c == 0) mode = 1;
+    else if (c + 1 < L.n_chunks) mode = 2;
+    else mode = 3;
+    if ((st = launch_gemm_store(mode, dz, L.chunk, n_rows, wt + v0, L.vpad, H, mpad, dX, acc, H,
+                                s)))
+      return st;
+  }
+  return NMCE_OK;
+}
+
+}  // extern "C"
+
+extern "C" int nmce_gemm_nt_bf16(const void* a, int64_t lda, const void* b, int64_t ldb,
+                                 int64_t m, int64_t n, int64_t k, void* c, int c_dtype,
+                                 int64_t ldc, void* stream) {
+  if (m < 0 || n < 0 || k < 0 || k % kBK != 0) return NMCE_EINVAL_SHAPE;
+  if (c_dtype != NMCE_BF16 && c_dtype != NMCE_F32) return NMCE_EINVAL_DTYPE;
+  if (m == 0 || n == 0) return NMCE_OK;
+  if (!operand_ok(a, lda) || !operand_ok(b, ldb) || lda < k || ldb < k) return NMCE_EINVAL_ALIGN;
+  if (!c || ldc < n) return NMCE_EINVAL_PTR;
+  if (m > (int64_t{1} << 30) || n > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
+  if (k == 0) return NMCE_EINVAL_SHAPE;
+  int st = configure_lds();
+  if (st) return st;
+  return launch_gemm_store(c_dtype == NMCE_BF16 ? 0 : 1, static_cast<const uint16_t*>(a), lda, m,
+                           static_cast<const uint16_t*>(b), ldb, n, k,
+                           static_cast<uint16_t*>(c), static_cast<float*>(c), ldc,
+                           static_cast<hipStream_t>(stream));
+}

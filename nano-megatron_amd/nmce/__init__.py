@@ -5,6 +5,10 @@ Public API (mirrors nano_megatron/cross_entropy.py and parallel.py):
 * ``vocab_parallel_cross_entropy(logits, target, vocab_start, vocab_end, ctx)``
   -> mean fp32 loss; backward yields the logits gradient.
 * ``_VocabParallelCrossEntropy`` -- the autograd Function (per-token loss).
+* ``lmhead_vocab_parallel_cross_entropy(hidden, weight, target, vocab_start,
+  vocab_end, ctx)`` -> the same loss of ``hidden @ weight.t()`` (the LM head of
+  model.py:192 fused in), never storing the logits; backward yields the hidden
+  and weight gradients.
 * ``ParallelContext`` / ``vocab_range`` / ``divide`` -- the topology fields and
   shard rule the loss reads.
 
@@ -17,12 +21,15 @@ from .cross_entropy import (
     validate_targets,
     vocab_parallel_cross_entropy,
 )
+from .lmhead import _LMHeadVocabParallelCrossEntropy, lmhead_vocab_parallel_cross_entropy
 from .parallel import ParallelContext, divide, vocab_range
 
 __all__ = [
+    "_LMHeadVocabParallelCrossEntropy",
     "_VocabParallelCrossEntropy",
     "ParallelContext",
     "divide",
+    "lmhead_vocab_parallel_cross_entropy",
     "validate_targets",
     "vocab_parallel_cross_entropy",
     "vocab_range",

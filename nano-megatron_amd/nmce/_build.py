@@ -23,7 +23,7 @@ INCLUDE_DIR = REPO_DIR / "include"
 BUILD_DIR = PROJECT_DIR / "_build"
 LIB_PATH = PKG_DIR / "libnmce.so"
 
-SOURCES = ["nmce_ce.hip"]
+SOURCES = ["nmce_ce.hip", "nmce_lmhead.hip"]
 
 ARCH = "gfx950"
 

@@ -66,19 +66,24 @@ def _as_rows(logits: torch.Tensor) -> torch.Tensor | None:
         return None
 
 
+def _check_target(target: torch.Tensor, lead_shape, device: torch.device) -> None:
+    """``target`` must be int64 on ``device`` with the token shape ``lead_shape``."""
+    if target.device != device:
+        raise RuntimeError(f"nmce: target on {target.device}, inputs on {device}")
+    if target.dtype != torch.int64:
+        raise TypeError(f"nmce: target must be int64, got {target.dtype}")
+    if tuple(target.shape) != tuple(lead_shape):
+        raise ValueError(
+            f"nmce: target shape {tuple(target.shape)} does not match the token shape "
+            f"{tuple(lead_shape)} of the inputs")
+
+
 def _check_inputs(logits: torch.Tensor, target: torch.Tensor, vocab_start: int,
                   vocab_end: int) -> None:
     if not logits.is_cuda:
         raise RuntimeError("nmce: logits must be on a ROCm device (there is no CPU path)")
-    if target.device != logits.device:
-        raise RuntimeError(f"nmce: target on {target.device}, logits on {logits.device}")
-    if target.dtype != torch.int64:
-        raise TypeError(f"nmce: target must be int64, got {target.dtype}")
+    _check_target(target, logits.shape[:-1], logits.device)
     _lib.dtype_code(logits.dtype)
-    if tuple(target.shape) != tuple(logits.shape[:-1]):
-        raise ValueError(
-            f"nmce: target shape {tuple(target.shape)} does not match logits "
-            f"{tuple(logits.shape)} without the vocabulary dimension")
     if vocab_end - vocab_start != logits.shape[-1]:
         raise ValueError(
             f"nmce: logits hold {logits.shape[-1]} vocabulary entries but the shard "

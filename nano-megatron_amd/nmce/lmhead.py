@@ -1,0 +1,178 @@
+"""Fused LM head + vocabulary-parallel cross entropy on gfx950 HIP kernels.
+
+Drop-in for the tail of nano_megatron's ``GPT.forward`` (model.py:277-281):
+
+    logits = self.lm_head(self.final_norm(h))          # x @ W.t(), model.py:192
+    return vocab_parallel_cross_entropy(logits, labels, start, end, self.ctx)
+
+becomes
+
+    return lmhead_vocab_parallel_cross_entropy(x, W, labels, start, end, self.ctx)
+
+with ``x`` the (already TP-mapped, model.py:188-191) hidden state and ``W`` the
+LM head's vocabulary shard ``[V/tp, H]``. The loss and its gradients with
+respect to ``x`` and ``W`` are those of the two-step reference, but the
+``[tokens, V/tp]`` logits are never stored: the forward keeps two floats per
+token and the backward recomputes the logits one vocabulary chunk at a time.
+
+Numerics: the reference runs the projection in bf16 under autocast
+(model.py:255-257), so its logits are rounded to bf16 before the loss; here
+they stay fp32 from the MFMA accumulators into the softmax. The logit
+gradient is rounded to bf16 before the two backward products, as the
+reference's autocast matmul backward consumes a bf16 gradient.
+
+Both ``x`` and ``W`` must be bf16 on a ROCm device; there is no CPU path.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from .cross_entropy import _check_target, _exchange_stats, _launch, launch_target_check
+
+# Default vocabulary rows per backward chunk: the chunk's logit gradient is
+# held twice in bf16 (2 * 2 * tokens * chunk bytes).
+DEFAULT_VOCAB_CHUNK = 16384
+
+_ALIGN = 64  # hidden size granularity of the GEMM kernels
+
+
+def _padded_hidden(t: torch.Tensor, hp: int) -> torch.Tensor:
+    """``t`` [rows, H] as a contiguous [rows, hp] bf16 tensor (zero columns appended)."""
+    rows, h = t.shape
+    if h == hp and t.is_contiguous() and t.data_ptr() % 16 == 0:
+        return t
+    out = torch.zeros((rows, hp), dtype=t.dtype, device=t.device)
+    out[:, :h] = t
+    return out
+
+
+def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
+    return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
+    """Per-token loss of ``hidden @ weight.t()`` over a vocabulary shard.
+
+    ``forward(hidden, weight, target, vocab_start, vocab_end, group, world_size,
+    vocab_chunk=None)``: ``hidden`` is ``[..., H]`` bf16, ``weight`` is
+    ``[vocab_end - vocab_start, H]`` bf16 and ``target`` has ``hidden``'s
+    leading shape. Returns the fp32 per-token loss (cross_entropy.py:45).
+    ``backward`` returns the bf16 gradients of ``hidden`` (this shard's
+    contribution) and ``weight``.
+    """
+
+    @staticmethod
+    def forward(ctx, hidden, weight, target, vocab_start, vocab_end, group, world_size,
+                vocab_chunk=None):
+        if not (hidden.is_cuda and weight.is_cuda):
+            raise RuntimeError("nmce: hidden and weight must be on a ROCm device "
+                               "(there is no CPU path)")
+        if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+            raise TypeError("nmce: the fused LM head computes in bf16; got hidden "
+                            f"{hidden.dtype}, weight {weight.dtype}")
+        if weight.dim() != 2 or hidden.shape[-1] != weight.shape[1]:
+            raise ValueError(f"nmce: hidden {tuple(hidden.shape)} and weight "
+                             f"{tuple(weight.shape)} do not share the hidden size")
+        if weight.shape[0] != vocab_end - vocab_start:
+            raise ValueError(f"nmce: weight holds {weight.shape[0]} vocabulary rows but the "
+                             f"shard [{vocab_start}, {vocab_end}) has {vocab_end - vocab_start}")
+        _check_target(target, hidden.shape[:-1], hidden.device)
+        lib = _lib.load()
+        dev = hidden.device
+        stream = _lib.stream_handle(dev)
+        H = hidden.shape[-1]
+        V = weight.shape[0]
+        hp = (H + _ALIGN - 1) // _ALIGN * _ALIGN
+        x = _padded_hidden(hidden.reshape(-1, H), hp)
+        w = _padded_hidden(weight, hp)
+        n = x.shape[0]
+        tgt = target.reshape(-1)
+        if not tgt.is_contiguous():
+            tgt = tgt.contiguous()
+
+        out = torch.empty((3, n), dtype=torch.float32, device=dev)  # loss, max, sumexp
+        loss, row_stat = out[0], out[1:]
+        local = torch.empty((3, n), dtype=torch.float32, device=dev)
+        ws = _workspace(lib.nmce_lmhead_ce_fwd_workspace_bytes(n, hp, V), dev)
+        _launch("nmce_lmhead_ce_fwd_stats", lib.nmce_lmhead_ce_fwd_stats, x.data_ptr(),
+                w.data_ptr(), _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), vocab_start,
+                local[0].data_ptr(), local[1].data_ptr(), local[2].data_ptr(), ws.data_ptr(),
+                ws.numel(), stream)
+        if world_size == 1:
+            stats, stride = local, 3 * n
+        else:
+            stats, stride = _exchange_stats(local, group, world_size), 3 * n
+        base = stats.data_ptr()
+        _launch("nmce_ce_combine", lib.nmce_ce_combine, base, base + 4 * n, base + 8 * n,
+                world_size, stride, n, loss.data_ptr(), row_stat[0].data_ptr(),
+                row_stat[1].data_ptr(), stream)
+
+        ctx.vocab_start = vocab_start
+        ctx.vocab_chunk = DEFAULT_VOCAB_CHUNK if vocab_chunk is None else int(vocab_chunk)
+        ctx.hidden_shape = hidden.shape
+        ctx.H = H
+        ctx.save_for_backward(x, w, tgt, row_stat)
+        return loss.view(target.shape)
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        x, w, tgt, row_stat = ctx.saved_tensors
+        lib = _lib.load()
+        dev = x.device
+        n, hp = x.shape
+        V = w.shape[0]
+        go = grad_output
+        if go.dtype != torch.float32:
+            go = go.float()
+        if go.numel() > 0 and all(s == 0 for s in go.stride()):
+            gstride = 0  # expanded scalar, e.g. from loss.mean()
+        else:
+            go = go.reshape(-1)
+            if not go.is_contiguous():
+                go = go.contiguous()
+            gstride = 1
+        dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
+        dw = torch.empty((V, hp), dtype=torch.bfloat16, device=dev)
+        ws = _workspace(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, hp, V, ctx.vocab_chunk), dev)
+        _launch("nmce_lmhead_ce_bwd", lib.nmce_lmhead_ce_bwd, x.data_ptr(), w.data_ptr(),
+                _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), ctx.vocab_start,
+                row_stat[0].data_ptr(), row_stat[1].data_ptr(), go.data_ptr(), gstride,
+                dx.data_ptr(), dw.data_ptr(), ctx.vocab_chunk, ws.data_ptr(), ws.numel(),
+                _lib.stream_handle(dev))
+        H = ctx.H
+        if hp != H:
+            dx = dx[:, :H]
+            dw = dw[:, :H].contiguous()
+        return (dx.reshape(ctx.hidden_shape), dw, None, None, None, None, None, None)
+
+
+def lmhead_vocab_parallel_cross_entropy(
+    hidden: torch.Tensor,
+    weight: torch.Tensor,
+    target: torch.Tensor,
+    vocab_start: int,
+    vocab_end: int,
+    ctx,
+    *,
+    vocab_chunk: int | None = None,
+    validate: bool = True,
+) -> torch.Tensor:
+    """Mean cross-entropy of ``hidden @ weight.t()`` against ``target``.
+
+    Equals ``vocab_parallel_cross_entropy(hidden @ weight.t(), target,
+    vocab_start, vocab_end, ctx)`` (cross_entropy.py:68-85 after
+    model.py:192) without storing the logits. ``hidden`` is ``[b, s, H]`` (or
+    ``[tokens, H]``), ``weight`` is ``[V/tp, H]``, both bf16; returns a 0-dim
+    fp32 tensor. Same ``ValueError`` as the reference for an out-of-range
+    target.
+    """
+    vocab_size = ctx.tp_size * (vocab_end - vocab_start)
+    _check_target(target, hidden.shape[:-1], hidden.device)
+    pending = launch_target_check(target, vocab_size) if validate else None
+    loss = _LMHeadVocabParallelCrossEntropy.apply(
+        hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, vocab_chunk)
+    if pending is not None:
+        pending.raise_if_bad()
+    return loss.mean()

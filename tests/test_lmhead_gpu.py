@@ -1,0 +1,419 @@
+"""GPU parity of the fused LM head + cross entropy (libnmce HIP kernels).
+
+The fused path computes the loss of ``hidden @ weight.t()`` (model.py:192
+followed by cross_entropy.py:16-85) without storing the logits. Checks:
+
+* the GEMM core (``nmce_gemm_nt_bf16``) against an fp64 product of the same
+  bf16 values: fp32 output within 1e-5 of the largest |entry| of that row's
+  dot-product scale, bf16 output within one bf16 ulp plus that floor;
+* per-token loss against the fp64 closed form ``logsumexp(z) - z_t`` on the
+  same bf16 inputs (small shapes: every token; workload shapes: seeded token
+  subsets): within 1e-5 relative (the logits are exact bf16 products summed
+  in fp32, so the loss keeps fp32 accuracy);
+* the hidden / weight gradients against the fp64 closed form
+  ``dZ = (softmax - onehot) * g``, ``dH = dZ W``, ``dW = dZ^T H``. The kernels
+  round dZ to bf16 before the two products (as the reference's autocast
+  backward does) and write bf16 results, so each gradient is held to a
+  norm-relative error of 4e-3 against the exact product (bf16 rounding alone
+  gives about 1.5e-3), and every element to the same product taken with dZ
+  rounded to bf16: within one bf16 rounding of the result (2^-8 relative) plus
+  2^-7 * sum |dZ||W| (the kernels' fp32 dZ and the fp64 dZ can round to
+  neighbouring bf16 values at ties: one ulp, at most 2^-7 relative, per term);
+* shard masking / offsets through a locally combined two-shard split, the
+  chunked backward against the one-chunk backward, ragged sizes, and the
+  drop-in wrapper against the unfused loss on the stored logits.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ce_oracle
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _lib():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    from nmce import _lib as L
+    lib = L.load()
+    print(f"[gpu] libnmce {lib.nmce_version():#x} on {torch.cuda.get_device_name(0)}",
+          flush=True)
+    return lib
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def make_inputs(n, h, v, seed=0, x_std=1.0, w_std=0.02, v_total=None):
+    g = _gen(seed)
+    x = (torch.randn(n, h, generator=g) * x_std).to(torch.bfloat16)
+    w = (torch.randn(v, h, generator=g) * w_std).to(torch.bfloat16)
+    t = torch.randint(0, v_total or v, (n,), generator=g)
+    return x, w, t
+
+
+def _bf16_round(a: np.ndarray) -> np.ndarray:
+    return torch.from_numpy(np.ascontiguousarray(a)).float().to(torch.bfloat16).double().numpy()
+
+
+class GradRef:
+    """Exact fp64 gradient ``a @ b`` plus the same product with ``a`` (dZ)
+    rounded to bf16, and the l1 product |a| @ |b| that bounds rounding flips."""
+
+    def __init__(self, a: np.ndarray, b: np.ndarray):
+        self.exact = a @ b
+        ab = _bf16_round(a)
+        self.rounded = ab @ b
+        self.l1 = np.abs(ab) @ np.abs(b)
+
+
+def fp64_reference(x, w, t, vstart=0, g=None):
+    """Closed-form loss and gradients in fp64 (numpy) on the bf16 values.
+    Returns (loss, dz, GradRef for dH, GradRef for dW)."""
+    X = x.double().numpy()
+    W = w.double().numpy()
+    Z = X @ W.T
+    n, v = Z.shape
+    g = np.full(n, 1.0 / n) if g is None else np.asarray(g, dtype=np.float64)
+    m = Z.max(axis=1, keepdims=True)
+    e = np.exp(Z - m)
+    s = e.sum(axis=1, keepdims=True)
+    tl = t.numpy() - vstart
+    own = (tl >= 0) & (tl < v)
+    zt = np.where(own, Z[np.arange(n), np.clip(tl, 0, v - 1)], 0.0)
+    loss = np.log(s[:, 0]) + m[:, 0] - zt
+    dz = e / s
+    dz[np.arange(n)[own], tl[own]] -= 1.0
+    dz *= g[:, None]
+    return loss, dz, GradRef(dz, W), GradRef(dz.T.copy(), X)
+
+
+def check_grad(got, ref: GradRef, what, norm_tol=4e-3):
+    got = np.asarray(got, dtype=np.float64)
+    nrel = np.linalg.norm(got - ref.exact) / max(np.linalg.norm(ref.exact), 1e-300)
+    assert nrel <= norm_tol, f"{what}: norm-relative error {nrel:.3e} > {norm_tol}"
+    # output rounding (half a bf16 ulp, <= 2^-8 relative) plus one bf16 ulp
+    # (<= 2^-7 relative) on any dZ term whose rounding flipped at a tie
+    bound = 2.0 ** -8 * np.abs(ref.rounded) + 2.0 ** -7 * ref.l1 + 1e-30
+    bad = np.abs(got - ref.rounded) > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} elements off; first at "
+                           f"{np.argwhere(bad)[0]}: {got[bad][0]} vs {ref.rounded[bad][0]}")
+    return nrel
+
+
+def run_fused(x, w, t, vstart=0, vchunk=None, g=None, tp_stats=None):
+    """Forward stats + combine + backward through the C ABI. Returns
+    (loss, dx, dw) as numpy; ``tp_stats`` returns the raw shard stats instead."""
+    from nmce import _lib as L
+    lib = L.load()
+    n, h = x.shape
+    v = w.shape[0]
+    xd, wd = x.to(DEV), w.to(DEV)
+    td = t.to(DEV)
+    stream = L.stream_handle(torch.device(DEV))
+    stats = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    ws = torch.empty(max(lib.nmce_lmhead_ce_fwd_workspace_bytes(n, h, v), 16), dtype=torch.uint8,
+                     device=DEV)
+    L.check(lib.nmce_lmhead_ce_fwd_stats(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, v,
+                                         td.data_ptr(), vstart, stats[0].data_ptr(),
+                                         stats[1].data_ptr(), stats[2].data_ptr(), ws.data_ptr(),
+                                         ws.numel(), stream), "fwd_stats")
+    if tp_stats is not None:
+        return stats
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    b = stats.data_ptr()
+    L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, 1, 3 * n, n, out[0].data_ptr(),
+                                out[1].data_ptr(), out[2].data_ptr(), stream), "combine")
+    if g is None:
+        go = torch.full((1,), 1.0 / n, dtype=torch.float32, device=DEV)
+        gs = 0
+    else:
+        go = torch.as_tensor(g, dtype=torch.float32).to(DEV)
+        gs = 1
+    dx = torch.empty((n, h), dtype=torch.bfloat16, device=DEV)
+    dw = torch.empty((v, h), dtype=torch.bfloat16, device=DEV)
+    chunk = 0 if vchunk is None else vchunk
+    ws2 = torch.empty(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, h, v, chunk), dtype=torch.uint8,
+                      device=DEV)
+    L.check(lib.nmce_lmhead_ce_bwd(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, v,
+                                   td.data_ptr(), vstart, out[1].data_ptr(), out[2].data_ptr(),
+                                   go.data_ptr(), gs, dx.data_ptr(), dw.data_ptr(), chunk,
+                                   ws2.data_ptr(), ws2.numel(), stream), "bwd")
+    torch.cuda.synchronize()
+    return (out[0].cpu().numpy(), dx.float().cpu().numpy(), dw.float().cpu().numpy())
+
+
+# ---------------------------------------------------------------------------
+# GEMM core
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (512, 768, 256), (300, 520, 128),
+                                   (1000, 777, 320), (1, 3, 64), (2048, 1024, 4096)])
+@pytest.mark.parametrize("out", ["f32", "bf16"])
+def test_gemm_nt(m, n, k, out):
+    from nmce import _lib as L
+    lib = L.load()
+    print(f"[gemm] m={m} n={n} k={k} out={out}", flush=True)
+    g = _gen(m * 7 + n * 3 + k)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    b = torch.randn(n, k, generator=g).to(torch.bfloat16)
+    ad, bd = a.to(DEV), b.to(DEV)
+    dt = torch.float32 if out == "f32" else torch.bfloat16
+    c = torch.full((m, n), float("nan"), dtype=dt, device=DEV)
+    L.check(lib.nmce_gemm_nt_bf16(ad.data_ptr(), k, bd.data_ptr(), k, m, n, k, c.data_ptr(),
+                                  L.NMCE_F32 if out == "f32" else L.NMCE_BF16, n,
+                                  L.stream_handle(torch.device(DEV))), "gemm")
+    torch.cuda.synchronize()
+    ref = a.double().numpy() @ b.double().numpy().T
+    got = c.float().cpu().numpy().astype(np.float64)
+    scale = np.sqrt(k) * 4.0  # |a||b| scale of one dot product of N(0,1) values
+    err = np.abs(got - ref)
+    bound = 1e-5 * scale + (2.0 ** -8 * np.abs(ref) if out == "bf16" else 0.0)
+    assert np.isfinite(got).all()
+    assert (err <= bound).all(), f"max err {err.max():.3e} (bound {np.min(bound):.3e})"
+
+
+def test_gemm_rejects_bad_k():
+    from nmce import _lib as L
+    lib = L.load()
+    a = torch.zeros(64, 100, dtype=torch.bfloat16, device=DEV)
+    st = lib.nmce_gemm_nt_bf16(a.data_ptr(), 100, a.data_ptr(), 100, 64, 64, 100, a.data_ptr(),
+                               L.NMCE_F32, 64, None)
+    assert st == -2
+
+
+# ---------------------------------------------------------------------------
+# Fused loss: small shapes against the fp64 closed form
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,h,v", [(256, 64, 256), (300, 128, 1000), (77, 192, 513),
+                                   (512, 256, 2048), (1, 64, 5)])
+def test_fused_small(n, h, v):
+    print(f"[fused] n={n} h={h} v={v}", flush=True)
+    x, w, t = make_inputs(n, h, v, seed=n + v, x_std=1.0, w_std=0.5)
+    loss, dx, dw = run_fused(x, w, t)
+    rl, _, rdx, rdw = fp64_reference(x, w, t)
+    np.testing.assert_allclose(loss, rl, rtol=1e-5, atol=1e-6)
+    check_grad(dx, rdx, "dH")
+    check_grad(dw, rdw, "dW")
+
+
+def test_fused_per_token_grad_output():
+    n, h, v = 300, 128, 1000
+    x, w, t = make_inputs(n, h, v, seed=3, w_std=0.5)
+    g = np.random.default_rng(3).uniform(0.1, 2.0, n).astype(np.float32)
+    loss, dx, dw = run_fused(x, w, t, g=g)
+    rl, _, rdx, rdw = fp64_reference(x, w, t, g=g.astype(np.float64))
+    np.testing.assert_allclose(loss, rl, rtol=1e-5, atol=1e-6)
+    check_grad(dx, rdx, "dH")
+    check_grad(dw, rdw, "dW")
+
+
+@pytest.mark.parametrize("chunk", [256, 512, 768])
+def test_fused_chunked_backward_matches(chunk):
+    n, h, v = 384, 128, 2000
+    x, w, t = make_inputs(n, h, v, seed=11, w_std=0.5)
+    _, dx1, dw1 = run_fused(x, w, t, vchunk=None)
+    _, dx2, dw2 = run_fused(x, w, t, vchunk=chunk)
+    # dW rows are computed identically per chunk; dH sums chunk partials in fp32.
+    np.testing.assert_array_equal(dw1, dw2)
+    rl, _, rdx, _ = fp64_reference(x, w, t)
+    check_grad(dx2, rdx, f"dH chunk {chunk}")
+    check_grad(dx1, rdx, "dH one chunk")
+
+
+def test_fused_two_shards_combined():
+    """TP=2 split of the vocabulary, shards combined locally: same loss and the
+    same gradients (dW rows per shard, dH summed) as the full vocabulary."""
+    from nmce import _lib as L
+    lib = L.load()
+    n, h, v = 300, 128, 1024
+    x, w, t = make_inputs(n, h, v, seed=5, w_std=0.5)
+    half = v // 2
+    stats = [run_fused(x, w[r * half:(r + 1) * half], t, vstart=r * half, tp_stats=True)
+             for r in range(2)]
+    stack = torch.stack(stats)  # [2, 3, n]
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    b = stack.data_ptr()
+    L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, 2, 3 * n, n, out[0].data_ptr(),
+                                out[1].data_ptr(), out[2].data_ptr(),
+                                L.stream_handle(torch.device(DEV))), "combine")
+    rl, _, rdx, rdw = fp64_reference(x, w, t)
+    np.testing.assert_allclose(out[0].cpu().numpy(), rl, rtol=1e-5, atol=1e-6)
+    # each shard owns about half the targets
+    own0 = (t < half).float().mean().item()
+    assert 0.3 < own0 < 0.7
+    dxs, dws = [], []
+    for r in range(2):
+        xd, wd = x.to(DEV), w[r * half:(r + 1) * half].contiguous().to(DEV)
+        dx = torch.empty((n, h), dtype=torch.bfloat16, device=DEV)
+        dw = torch.empty((half, h), dtype=torch.bfloat16, device=DEV)
+        go = torch.full((1,), 1.0 / n, dtype=torch.float32, device=DEV)
+        td = t.to(DEV)
+        ws = torch.empty(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, h, half, 0), dtype=torch.uint8,
+                         device=DEV)
+        L.check(lib.nmce_lmhead_ce_bwd(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, half,
+                                       td.data_ptr(), r * half, out[1].data_ptr(),
+                                       out[2].data_ptr(), go.data_ptr(), 0, dx.data_ptr(),
+                                       dw.data_ptr(), 0, ws.data_ptr(), ws.numel(),
+                                       L.stream_handle(torch.device(DEV))), "bwd")
+        dxs.append(dx.float().cpu().numpy())
+        dws.append(dw.float().cpu().numpy())
+    check_grad(np.concatenate(dws), rdw, "dW (two shards)")
+    check_grad(dxs[0] + dxs[1], rdx, "dH (sum of shards)")
+
+
+def test_fused_ragged_hidden_is_padded():
+    """H = 100 is not a multiple of 64: the wrapper pads with zero columns."""
+    import nmce
+    n, h, v = 128, 100, 700
+    x, w, t = make_inputs(n, h, v, seed=9, w_std=0.5)
+    xd = x.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v,
+                                                    nmce.ParallelContext.single())
+    loss.backward()
+    rl, _, rdx, rdw = fp64_reference(x, w, t)
+    assert abs(loss.item() - rl.mean()) <= 1e-5 * abs(rl.mean())
+    assert xd.grad.shape == (n, h) and wd.grad.shape == (v, h)
+    check_grad(xd.grad.float().cpu().numpy(), rdx, "dH")
+    check_grad(wd.grad.float().cpu().numpy(), rdw, "dW")
+
+
+def test_dropin_matches_unfused_on_stored_logits():
+    """lmhead_vocab_parallel_cross_entropy(x, W, t) == vocab_parallel_cross_entropy(x W^T, t)."""
+    import nmce
+    b, s, h, v = 2, 160, 256, 3000
+    x, w, t = make_inputs(b * s, h, v, seed=21, w_std=0.3)
+    ctx = nmce.ParallelContext.single()
+    xd = x.view(b, s, h).to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    td = t.view(b, s).to(DEV)
+    loss_f = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, td, 0, v, ctx)
+    loss_f.backward()
+    xu = x.view(b, s, h).to(DEV).float()
+    wu = w.to(DEV).float()
+    logits = torch.matmul(xu, wu.t().contiguous()).requires_grad_(True)
+    loss_u = nmce.vocab_parallel_cross_entropy(logits, td, 0, v, ctx, inplace=False)
+    loss_u.backward()
+    assert loss_f.dtype == torch.float32 and loss_f.dim() == 0
+    assert abs(loss_f.item() - loss_u.item()) <= 1e-5 * abs(loss_u.item())
+    # the unfused path's fp32 logit gradient, through the same two products
+    dz = logits.grad.reshape(b * s, v).double().cpu().numpy()
+    check_grad(xd.grad.float().cpu().numpy().reshape(b * s, h),
+               GradRef(dz, w.double().numpy()), "dH vs unfused")
+    check_grad(wd.grad.float().cpu().numpy(), GradRef(dz.T.copy(), x.double().numpy()),
+               "dW vs unfused")
+
+
+def test_dropin_rejects_bad_target():
+    import nmce
+    x, w, t = make_inputs(64, 64, 100, seed=1)
+    t[5] = 100
+    with pytest.raises(ValueError, match="outside the model vocabulary"):
+        nmce.lmhead_vocab_parallel_cross_entropy(x.to(DEV), w.to(DEV), t.to(DEV), 0, 100,
+                                                 nmce.ParallelContext.single())
+
+
+# ---------------------------------------------------------------------------
+# Workload shapes: token / vocabulary subsets against fp32-on-GPU references
+# ---------------------------------------------------------------------------
+
+def _subset_reference(xd, wd, td, rows, g):
+    """Loss and a dH GradRef for token subset ``rows`` (fp64, full vocabulary)."""
+    zs = (xd[rows].double() @ wd.double().t())
+    lse = torch.logsumexp(zs, dim=1)
+    loss = lse - zs[torch.arange(len(rows), device=DEV), td[rows]]
+    p = torch.exp(zs - lse[:, None])
+    p[torch.arange(len(rows), device=DEV), td[rows]] -= 1.0
+    return loss.cpu().numpy(), _grad_ref_gpu(p * g, wd.double())
+
+
+def _grad_ref_gpu(a: torch.Tensor, b: torch.Tensor) -> GradRef:
+    ref = GradRef.__new__(GradRef)
+    ref.exact = (a @ b).cpu().numpy()
+    ab = a.float().to(torch.bfloat16).double()
+    ref.rounded = (ab @ b).cpu().numpy()
+    ref.l1 = (ab.abs() @ b.abs()).cpu().numpy()
+    return ref
+
+
+def _dw_subset_reference(xd, wd, td, vrows, lse_all, g):
+    """dW GradRef for rows ``vrows`` in fp64, given every token's fp64 logsumexp."""
+    zc = xd.double() @ wd[vrows].double().t()                       # [N, |vrows|]
+    p = torch.exp(zc - lse_all[:, None])
+    onehot = (td[:, None] == vrows[None, :]).double()
+    return _grad_ref_gpu(((p - onehot) * g).t().contiguous(), xd.double())
+
+
+def _lse_all(xd, wd, chunk=1024):
+    out = []
+    wt = wd.double().t().contiguous()
+    for i in range(0, xd.shape[0], chunk):
+        out.append(torch.logsumexp(xd[i:i + chunk].double() @ wt, dim=1))
+    return torch.cat(out)
+
+
+@pytest.mark.parametrize("cfg", ["c4", "c5"])
+def test_fused_workload(cfg):
+    """c4: hidden [16384, 4096] ~ N(0,1), W [128256, 4096] ~ N(0, 0.02^2), uniform
+    targets. c5: hidden [16384, 3072], W [256000, 3072] ~ N(0, 0.05^2) with 64
+    rows x30, Zipf(1.1) targets (logits far beyond +-60)."""
+    import nmce
+    from nmce import _lib as L
+    lib = L.load()
+    g = torch.Generator(device=DEV).manual_seed(0)
+    if cfg == "c4":
+        n, h, v = 16384, 4096, 128256
+        x = torch.randn(n, h, device=DEV, generator=g).to(torch.bfloat16)
+        w = (torch.randn(v, h, device=DEV, generator=g) * 0.02).to(torch.bfloat16)
+        t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    else:
+        n, h, v = 16384, 3072, 256000
+        x = torch.randn(n, h, device=DEV, generator=g).to(torch.bfloat16)
+        wf = torch.randn(v, h, device=DEV, generator=g) * 0.05
+        hot = torch.randperm(v, device=DEV, generator=g)[:64]
+        wf[hot] *= 30.0
+        w = wf.to(torch.bfloat16)
+        del wf
+        ranks = torch.arange(1, v + 1, device=DEV, dtype=torch.float64)
+        t = torch.multinomial((ranks ** -1.1).float(), n, replacement=True, generator=g)
+    print(f"[fused-workload] {cfg} n={n} h={h} v={v}", flush=True)
+    ctx = nmce.ParallelContext.single()
+    xd = x.clone().requires_grad_(True)
+    wd = w.clone().requires_grad_(True)
+    per_tok = nmce._LMHeadVocabParallelCrossEntropy.apply(xd, wd, t, 0, v, None, 1, None)
+    loss = per_tok.mean()
+    loss.backward()
+    torch.cuda.synchronize()
+    gval = 1.0 / n
+    rows = torch.randperm(n, device=DEV, generator=g)[:256]
+    rl, rdx = _subset_reference(x, w, t, rows, gval)
+    got = per_tok[rows].detach().cpu().numpy()
+    np.testing.assert_allclose(got, rl, rtol=1e-5, atol=1e-5)
+    check_grad(xd.grad[rows].float().cpu().numpy(), rdx, f"{cfg} dH rows")
+    lse = _lse_all(x, w)
+    # the weight rows of the most frequent targets plus a random sample
+    vrows = torch.cat([torch.bincount(t, minlength=v).topk(8).indices,
+                       torch.randperm(v, device=DEV, generator=g)[:56]])
+    if cfg == "c5":
+        vrows = torch.cat([vrows, hot[:8]])
+    rdw = _dw_subset_reference(x, w, t, vrows, lse, gval)
+    check_grad(wd.grad[vrows].float().cpu().numpy(), rdw, f"{cfg} dW rows")
+    # mean loss within 1e-3 relative of the fp64 mean over all tokens
+    zt = (x.double() * w[t].double()).sum(dim=1)
+    ref_mean = (lse - zt).mean().item()
+    assert abs(loss.item() - ref_mean) <= 1e-5 * abs(ref_mean)
+    if cfg == "c5":
+        zmax = 0.0
+        for i in range(0, n, 2048):
+            zmax = max(zmax, (x[i:i + 2048].float() @ w[hot].float().t()).abs().max().item())
+        print(f"[fused-workload] c5 max |logit| on the scaled rows: {zmax:.1f}", flush=True)
+        assert zmax > 60.0
