@@ -1,14 +1,20 @@
 #!/usr/bin/env python3
 """Benchmark of the vocabulary-parallel cross entropy on one MI355X.
 
-    python bench.py [--steps K] [--warmup W] [--workload c2|c3|c1] [--gpus 1]
+    python bench.py [--steps K] [--warmup W] [--workload c2|c3|c1|c4|c5] [--gpus 1]
 
-A step is one forward + backward of the loss over one batch of synthetic
-logits already resident in HBM, through the drop-in
+Unfused workloads (c1-c3): a step is one forward + backward of the loss over
+one batch of synthetic logits already resident in HBM, through the drop-in
 ``nmce.vocab_parallel_cross_entropy`` exactly as nano-megatron's GPT.forward
 calls it (model.py:277-281): target validation, per-shard statistics, the
 cross-shard combine, ``loss.mean()``, ``loss.backward()`` with the gradient
 written in place into the (non-leaf) logits.
+
+Fused workloads (c4, c5): a step is one forward + backward of
+``nmce.lmhead_vocab_parallel_cross_entropy(hidden, weight, target, ...)``,
+the LM-head projection (model.py:192) and the loss without stored logits:
+target validation, the MFMA statistics GEMM, the combine, ``loss.mean()``
+and ``loss.backward()`` producing the hidden and weight gradients.
 
 Workloads:
   c2 (default)  TP=1, bf16 logits [8,2048,50304] ~ N(0,1), targets U[0,V)
@@ -17,13 +23,20 @@ Workloads:
                 the peer rank's statistics are computed once up front and
                 handed over by an emulated all-gather, the combine is local
   c1            fp32 [4,256,32000] ~ N(0,2^2) (the reference's CPU config)
+  c4            fused: hidden bf16 [16384,4096] ~ N(0,1), tied weight bf16
+                [128256,4096] ~ N(0,0.02^2), targets U[0,128256)
+  c5            fused stress: hidden [16384,3072], weight [256000,3072] ~
+                N(0,0.05^2) with 64 rows x30, Zipf(1.1) targets
 
-Prints one JSON line. ``roofline`` covers the dominant kernel: its
-algorithmic HBM bytes per launch (tokens x vocab x bytes read and written,
-plus per-token statistics) over its average launch time, measured with HIP
-events on the launch stream during the timed steps. ``cpu_baseline`` is the
-torch-CPU restatement of the reference's op sequence (oracle/ce_restate.py)
-timed on this host on a bounded sample of the same workload.
+Prints one JSON line. ``roofline`` covers the dominant kernel: for the
+unfused loss its algorithmic HBM bytes per launch (tokens x vocab x bytes
+read and written, plus per-token statistics), for the fused loss the
+algorithmic flops of the statistics GEMM (2 x tokens x vocab x hidden), over
+its average launch time measured with HIP events on the launch stream during
+the timed steps. The default run (c2) adds a ``fused`` object with the c4
+measurement. ``cpu_baseline`` is the torch-CPU restatement of the
+reference's op sequence (oracle/ce_restate.py) timed on this host on a
+bounded sample of the same workload.
 """
 
 from __future__ import annotations
@@ -42,6 +55,7 @@ sys.path.insert(0, str(ROOT / "nano-megatron_amd"))
 
 METRIC = "vocab-CE fwd+bwd tokens/s at 1 GPU; % HBM roofline (unfused) / % MFMA peak (fused)"
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, published
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, published
 
 WORKLOADS = {
     "c2": dict(desc="unfused TP=1, bf16 logits [8,2048,50304] ~ N(0,1), targets U[0,50304)",
@@ -51,6 +65,12 @@ WORKLOADS = {
                b=4, s=4096, v=64128, tp=2, rank=1, sigma=1.5, dtype="bf16"),
     "c1": dict(desc="fp32 logits [4,256,32000] ~ N(0,2^2), targets U[0,32000), TP=1",
                b=4, s=256, v=32000, tp=1, rank=0, sigma=2.0, dtype="f32"),
+    "c4": dict(desc="fused LM head + CE: hidden bf16 [16384,4096] ~ N(0,1), tied weight bf16 "
+                    "[128256,4096] ~ N(0,0.02^2), targets U[0,128256)",
+               fused=True, n=16384, h=4096, v=128256, w_std=0.02, hot_rows=0, zipf=None),
+    "c5": dict(desc="fused stress: hidden bf16 [16384,3072] ~ N(0,1), weight bf16 [256000,3072] "
+                    "~ N(0,0.05^2) with 64 rows x30, targets Zipf(1.1)",
+               fused=True, n=16384, h=3072, v=256000, w_std=0.05, hot_rows=64, zipf=1.1),
 }
 
 
@@ -67,6 +87,12 @@ def parse_args():
     p.add_argument("--calibrate-copy", action="store_true",
                    help="after timing, run one nmce_stream_copy of the logits slab (known "
                         "traffic) so a counter run can scale FETCH_SIZE / WRITE_SIZE")
+    p.add_argument("--no-fused", action="store_true",
+                   help="default (c2) run only: skip the added c4 fused measurement")
+    p.add_argument("--fused-steps", type=int, default=10,
+                   help="timed steps of the c4 measurement added to the default run")
+    p.add_argument("--vocab-chunk", type=int, default=None,
+                   help="fused backward: vocabulary rows per chunk (default: the library's)")
     return p.parse_args()
 
 
@@ -168,6 +194,173 @@ def cpu_baseline(wl: dict, rows: int) -> dict:
     }
 
 
+def fused_inputs(wl: dict, dev):
+    """Seeded hidden states, weight shard and targets of a fused workload
+    (the same generator sequence as the fused workload parity test)."""
+    import torch
+    g = torch.Generator(device=dev).manual_seed(0)
+    n, h, v = wl["n"], wl["h"], wl["v"]
+    x = torch.randn(n, h, device=dev, generator=g).to(torch.bfloat16)
+    wf = torch.randn(v, h, device=dev, generator=g) * wl["w_std"]
+    if wl["hot_rows"]:
+        hot = torch.randperm(v, device=dev, generator=g)[:wl["hot_rows"]]
+        wf[hot] *= 30.0
+    w = wf.to(torch.bfloat16)
+    del wf
+    if wl["zipf"]:
+        ranks = torch.arange(1, v + 1, device=dev, dtype=torch.float64)
+        t = torch.multinomial((ranks ** -wl["zipf"]).float(), n, replacement=True, generator=g)
+    else:
+        t = torch.randint(0, v, (n,), device=dev, generator=g)
+    return x, w, t
+
+
+def cpu_baseline_fused(wl: dict, rows: int) -> dict:
+    """The reference's op sequence for the LM head + loss under bf16 autocast
+    on torch-CPU (model.py:192 in bf16, cross_entropy.py on the fp32 upcast,
+    the matmul backward in bf16), on ``rows`` tokens at the full vocabulary:
+    1 warmup, then the median of up to 3 (fewer if one step exceeds 10 s)."""
+    import torch
+    from oracle import ce_restate as R
+
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = min(threads, int(os.environ["OMP_NUM_THREADS"]))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    h, v = wl["h"], wl["v"]
+    x = torch.randn(rows, h, generator=g).to(torch.bfloat16)
+    w = (torch.randn(v, h, generator=g) * wl["w_std"]).to(torch.bfloat16)
+    t = torch.randint(0, v, (rows,), generator=g)
+    go = torch.full((rows,), 1.0 / rows)
+
+    def step():
+        if torch.any(t < 0) or torch.any(t >= v):
+            raise ValueError("bad target")
+        logits = torch.matmul(x, w.t())
+        loss, saved = R.forward(logits, t, 0, v)
+        loss.mean()
+        dz = R.backward(saved, go).to(torch.bfloat16)
+        return torch.matmul(dz, w), torch.matmul(dz.t(), x)
+
+    t0 = time.perf_counter()
+    step()
+    first = time.perf_counter() - t0
+    times = []
+    for _ in range(3 if first < 10.0 else 1):
+        t0 = time.perf_counter()
+        step()
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": rows / med,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{rows} tokens x full vocab {v}, hidden {h}: bf16 x @ W^T, torch-CPU "
+                  f"restatement of cross_entropy.py fwd+bwd on the fp32 upcast, bf16 dX/dW "
+                  f"matmuls; median of {len(times)} after 1 warmup; host {host_cpu_model()}, "
+                  f"torch {torch.__version__}",
+        "ms_per_step": med * 1e3,
+    }
+
+
+def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
+    """Time the fused LM head + loss (fwd + bwd) on workload ``name``."""
+    import torch
+    import nmce
+    import nmce.cross_entropy as ce_mod
+
+    wl = WORKLOADS[name]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    x, w, t = fused_inputs(wl, dev)
+    n, h, v = wl["n"], wl["h"], wl["v"]
+    ctx = nmce.ParallelContext.single()
+    xp = x.requires_grad_(True)
+    wp = w.requires_grad_(True)
+
+    def step():
+        xp.grad = None  # zero_grad(set_to_none=True) between steps
+        wp.grad = None
+        loss = nmce.lmhead_vocab_parallel_cross_entropy(xp, wp, t, 0, v, ctx,
+                                                        vocab_chunk=args.vocab_chunk)
+        loss.backward()
+        return loss
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
+
+    timeline: list = []
+    ce_mod.kernel_timeline = timeline
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    ce_mod.kernel_timeline = None
+    per_call: dict[str, list[float]] = {}
+    for cname, s_ev, e_ev in timeline:
+        per_call.setdefault(cname, []).append(s_ev.elapsed_time(e_ev))
+    avg_ms = {k: sum(vs) / len(vs) for k, vs in per_call.items()}
+
+    gemm_flops = 2.0 * n * v * h
+    dominant = "nmce_lmhead_ce_fwd_stats"
+    achieved = gemm_flops / (avg_ms[dominant] * 1e-3) / 1e12
+    alg_flops = 3 * gemm_flops      # forward GEMM + the dX and dW GEMMs
+    exe_flops = 4 * gemm_flops      # plus the recomputation of the logits in backward
+    result = {
+        "metric": METRIC,
+        "value": n / (ms_per_step * 1e-3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": f"{name}: {wl['desc']}",
+            "tokens": n,
+            "hidden": h,
+            "vocab_local": v,
+            "tp": 1,
+            "path": "nmce.lmhead_vocab_parallel_cross_entropy fwd+bwd (logits never stored; "
+                    "bf16 MFMA, fp32 accumulate), target validation, dX and dW",
+        },
+        "roofline": {
+            "bound": "mfma",
+            "kernel": dominant,
+            "achieved": achieved,
+            "peak": MFMA_BF16_PEAK_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
+            "traffic": None,
+            "alg_flops_per_launch": gemm_flops,
+            "avg_launch_ms": avg_ms[dominant],
+        },
+        "kernels_ms": avg_ms,
+        "path_roofline": {
+            "alg_flops_per_step": alg_flops,
+            "executed_flops_per_step": exe_flops,
+            "frac_alg_wall": alg_flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+            "frac_executed_wall": exe_flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+        },
+        "device": torch.cuda.get_device_name(0),
+    }
+    del x, w, t, xp, wp
+    torch.cuda.empty_cache()
+    result["cpu_baseline"] = cpu_baseline_fused(wl, 128) if with_cpu else None
+    return result
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -181,6 +374,11 @@ def main() -> int:
     import nmce.cross_entropy as ce_mod
 
     wl = WORKLOADS[args.workload]
+    if wl.get("fused"):
+        result = run_fused(args, args.workload, args.steps, args.warmup,
+                           with_cpu=not args.no_cpu_baseline)
+        print(json.dumps(result), flush=True)
+        return 0
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     n = wl["b"] * wl["s"]
@@ -318,6 +516,10 @@ def main() -> int:
         result["cpu_baseline"] = cpu_baseline(wl, args.cpu_rows)
     else:
         result["cpu_baseline"] = None
+    if args.workload == "c2" and not args.no_fused:
+        # The metric's second half: the fused LM head + loss on c4.
+        result["fused"] = run_fused(args, "c4", args.fused_steps, 2,
+                                    with_cpu=not args.no_cpu_baseline)
     print(json.dumps(result), flush=True)
     return 0
 

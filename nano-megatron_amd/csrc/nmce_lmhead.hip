@@ -25,8 +25,10 @@
 // each 128x128 = 16 accumulators of 32x32), K in steps of 64. Operand tiles
 // move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (global_load_lds_dwordx4,
 // no VGPR staging), double-buffered, rows of 128 bytes with the 16-byte chunks
-// XOR-swizzled by (row & 7) so that the ds_read_b128 fragment reads are free
-// of bank conflicts. Workgroups are mapped to tiles so that each XCD (one L2)
+// XOR-swizzled by ((row >> 1) & 7). gfx950's LDS has 64 banks, so a
+// ds_read_b128 serves 16 lanes (16 consecutive rows of a fragment) per cycle;
+// this swizzle puts those 16 rows on 16 distinct 16-byte bank groups (row
+// parity picks the half of the banks, the swizzled chunk the group). Workgroups are mapped to tiles so that each XCD (one L2)
 // owns a contiguous band of tiles walked in groups that share operands.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -44,8 +46,14 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 constexpr int kBM = 256;          // tile rows (GEMM M)
 constexpr int kBN = 256;          // tile columns (GEMM N)
 constexpr int kBK = 64;           // K per stage (128 bytes of bf16 per row)
-constexpr int kWavesM = 2;
-constexpr int kWavesN = 2;
+#ifndef NMCE_LMHEAD_WAVES_M
+#define NMCE_LMHEAD_WAVES_M 2
+#endif
+#ifndef NMCE_LMHEAD_WAVES_N
+#define NMCE_LMHEAD_WAVES_N 4
+#endif
+constexpr int kWavesM = NMCE_LMHEAD_WAVES_M;
+constexpr int kWavesN = NMCE_LMHEAD_WAVES_N;
 constexpr int kThreads = 64 * kWavesM * kWavesN;
 constexpr int kWaveM = kBM / kWavesM;  // 128
 constexpr int kWaveN = kBN / kWavesN;  // 128
@@ -60,7 +68,10 @@ constexpr int kBlocksA = kBM / 8;
 constexpr int kBlocksB = kBN / 8;
 constexpr int kBlocksPerWave = (kBlocksA + kBlocksB) / (kWavesM * kWavesN);
 static_assert(kBlocksA % kBlocksPerWave == 0, "a wave loads blocks of one operand only");
-constexpr int kGroupM = 8;         // tile rows per raster group inside an XCD band
+#ifndef NMCE_LMHEAD_GROUP_M
+#define NMCE_LMHEAD_GROUP_M 8
+#endif
+constexpr int kGroupM = NMCE_LMHEAD_GROUP_M;  // tile rows per raster group inside an XCD band
 constexpr int kXcds = 8;
 constexpr float kMaxFloorL = -1.0e38f;
 
@@ -115,11 +126,10 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
 
   // ---- load plan: this wave fills kBlocksPerWave 1 KiB blocks per stage ----
   // Lane p of a block writes LDS bytes [16p, 16p+16): row p/8 of the block,
-  // physical chunk p%8, which holds logical chunk (p%8) ^ (row & 7).
+  // physical chunk p%8, which holds logical chunk (p%8) ^ ((row >> 1) & 7).
   const int first_block = wave * kBlocksPerWave;
   const bool load_a = first_block < kBlocksA;
   const int row_lane = lane >> 3;
-  const int chunk = (lane & 7) ^ row_lane;
   const char* gbase;
   int64_t ld_op, rows_op;
   int lds_op;
@@ -134,7 +144,9 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
   uint32_t goff[kBlocksPerWave];
 #pragma unroll
   for (int j = 0; j < kBlocksPerWave; ++j) {
-    int64_t r = (blk0 + j) * 8 + row_lane;
+    const int tile_row = (blk0 + j) * 8 + row_lane;
+    const int chunk = (lane & 7) ^ ((tile_row >> 1) & 7);
+    int64_t r = tile_row;
     if (r > rows_op - 1) r = rows_op - 1;
     goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
   }
@@ -158,34 +170,76 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
   const int b_row_off = kStageA + (wn * kWaveN + frow) * 128;
   int xo[4];
 #pragma unroll
-  for (int s = 0; s < 4; ++s) xo[s] = (((2 * s + fhalf) ^ (frow & 7)) << 4);
+  for (int s = 0; s < 4; ++s) xo[s] = (((2 * s + fhalf) ^ ((frow >> 1) & 7)) << 4);
 
-  const int64_t kt_n = K / kBK;
-  issue(0, 0);
-  wait_vmem();
-  __syncthreads();
-  for (int64_t kt = 0; kt < kt_n; ++kt) {
-    const int cur = static_cast<int>(kt & 1);
-    if (kt + 1 < kt_n) issue(cur ^ 1, (kt + 1) * kBK);
-    const char* st = lds + cur * kStage;
+  // Fragments of one K sub-step; two sets alternate so that the LDS reads of
+  // sub-step s+1 are in flight under the 16 MFMAs of sub-step s.
+  struct Frags {
+    bf16x8_t a[kFM];
+    bf16x8_t b[kFN];
+  };
+  auto load_frags = [&](const char* st, int s, Frags& f) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      bf16x8_t a[kFM], b[kFN];
+    for (int i = 0; i < kFM; ++i)
+      f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
 #pragma unroll
-      for (int i = 0; i < kFM; ++i)
-        a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
+    for (int j = 0; j < kFN; ++j)
+      f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
+  };
+  auto mma = [&](const Frags& f) {
+#pragma unroll
+    for (int i = 0; i < kFM; ++i)
 #pragma unroll
       for (int j = 0; j < kFN; ++j)
-        b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
+        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.c[i][j], 0, 0, 0);
+  };
+
+  // One sub-step of the pipeline: the LDS reads of the next fragments (8 of
+  // them) interleaved one per MFMA with the 16 MFMAs of the current ones, so
+  // that the compiler neither serialises them nor reuses registers early.
+  auto step = [&](const char* st_next, int s_next, Frags& next, const Frags& cur) {
+    load_frags(st_next, s_next, next);
+    mma(cur);
 #pragma unroll
-      for (int i = 0; i < kFM; ++i)
-#pragma unroll
-        for (int j = 0; j < kFN; ++j)
-          acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[i], b[j], acc.c[i][j], 0, 0, 0);
+    for (int i = 0; i < kFM + kFN; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
     }
+    __builtin_amdgcn_sched_group_barrier(0x008, kFM * kFN - (kFM + kFN), 0);
+  };
+
+  // Stage kt lives in LDS buffer kt & 1. Loads run one stage ahead: stage
+  // kt+2 is issued into buffer kt & 1 as soon as every wave has its last
+  // fragments of stage kt in registers. Past the end of K the loads repeat the
+  // last stage (in bounds, never read), which keeps the loop free of branches.
+  const int64_t kt_n = K / kBK;
+  auto k_at = [&](int64_t kt) { return (kt < kt_n ? kt : kt_n - 1) * kBK; };
+  issue(0, 0);
+  issue(1, k_at(1));
+  wait_vmem();
+  __syncthreads();
+  Frags f0, f1;
+  load_frags(lds, 0, f0);
+  for (int64_t kt = 0; kt + 1 < kt_n; ++kt) {
+    const char* st = lds + static_cast<int>(kt & 1) * kStage;
+    step(st, 1, f1, f0);
+    step(st, 2, f0, f1);
+    step(st, 3, f1, f0);
+    // Own loads of stage kt+1 done; the barrier then also covers every other
+    // wave's loads and every wave's LDS reads of stage kt.
     wait_vmem();
     __syncthreads();
+    issue(static_cast<int>(kt & 1), k_at(kt + 2));
+    step(lds + static_cast<int>((kt + 1) & 1) * kStage, 0, f0, f1);
   }
+  {
+    const char* st = lds + static_cast<int>((kt_n - 1) & 1) * kStage;
+    step(st, 1, f1, f0);
+    step(st, 2, f0, f1);
+    step(st, 3, f1, f0);
+    mma(f1);
+  }
+  wait_vmem();
 }
 
 // Row (within the wave's 128 rows) of accumulator fm, element e, for this lane:
