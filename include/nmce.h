@@ -170,6 +170,48 @@ int64_t nmce_lmhead_ce_bwd_workspace_bytes(int64_t n_rows, int64_t hidden_size,
                                            int64_t vocab_local, int64_t vocab_chunk);
 
 /*
+ * Backward workspace layout (all values in elements of int64), written to
+ * layout[0 .. NMCE_LMHEAD_LAYOUT_FIELDS-1]:
+ *   [0] total workspace bytes
+ *   [1] ldt      tokens rounded up to 64 (row stride of X^T and dZ^T)
+ *   [2] vpad     vocab_local rounded up to 256 (row stride of W^T)
+ *   [3] chunk    vocabulary rows per chunk (multiple of 256)
+ *   [4] n_chunks
+ *   [5] byte offset of X^T   bf16 [hidden_size, ldt], zero beyond n_rows
+ *   [6] byte offset of W^T   bf16 [hidden_size, vpad], zero beyond vocab_local
+ *   [7] byte offset of dZ^T  bf16 [chunk, ldt] of the current chunk
+ *   [8] byte offset of dZ    bf16 [n_rows, chunk] of the current chunk
+ *   [9] byte offset of the fp32 [n_rows, hidden_size] accumulator of
+ *       nmce_lmhead_ce_bwd (present when n_chunks > 1)
+ */
+#define NMCE_LMHEAD_LAYOUT_FIELDS 10
+int nmce_lmhead_ce_bwd_layout(int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                              int64_t vocab_chunk, int64_t* layout);
+
+/* Step 1 of a caller-driven backward: X^T and W^T into the workspace. */
+int nmce_lmhead_ce_bwd_prepare(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                               int64_t hidden_size, int64_t vocab_local, int64_t vocab_chunk,
+                               void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Step 2, once per chunk c (rows [c*chunk, c*chunk + chunk) of the shard):
+ * recompute that slice of the logits and write the logit gradient
+ *   dZ[r, j] = (exp(z[r, j] - g_max[r]) / g_sumexp[r]
+ *               - [j == target[r] - vocab_start]) * grad_output[r*gout_stride]
+ * as bf16 into the workspace's dZ^T and dZ (zeros in their padding). The
+ * caller then forms grad_weight rows = dZ^T_c X and grad_hidden += dZ_c W_c
+ * (e.g. with a library GEMM on X^T and W^T) before the next chunk overwrites
+ * them. This is the fused part of cross_entropy.py:53-65 + the matmul
+ * backward of model.py:192.
+ */
+int nmce_lmhead_ce_bwd_dz(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                          int64_t hidden_size, int64_t vocab_local, const int64_t* target,
+                          int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                          const float* grad_output, int64_t gout_stride, int64_t vocab_chunk,
+                          int64_t chunk_index, void* workspace, int64_t workspace_bytes,
+                          void* stream);
+
+/*
  * Backward of the fused LM head + loss (cross_entropy.py:53-65 followed by
  * the matmul backward of model.py:192):
  *   dZ[r, j]        = (exp(z[r, j] - g_max[r]) / g_sumexp[r]

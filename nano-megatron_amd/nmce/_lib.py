@@ -44,7 +44,13 @@ SIGNATURES: dict[str, tuple] = {
     "nmce_lmhead_ce_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64,
                                     _p, _p, _i64, _p, _i64, _p]),
     "nmce_gemm_nt_bf16": (_c_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _p, _c_int, _i64, _p]),
+    "nmce_lmhead_ce_bwd_layout": (_c_int, [_i64, _i64, _i64, _i64, _p]),
+    "nmce_lmhead_ce_bwd_prepare": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p]),
+    "nmce_lmhead_ce_bwd_dz": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p,
+                                       _i64, _i64, _i64, _p, _i64, _p]),
 }
+
+NMCE_LMHEAD_LAYOUT_FIELDS = 10
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -33,7 +33,16 @@ from .cross_entropy import _check_target, _exchange_stats, _launch, launch_targe
 
 # Default vocabulary rows per backward chunk: the chunk's logit gradient is
 # held twice in bf16 (2 * 2 * tokens * chunk bytes).
-DEFAULT_VOCAB_CHUNK = 16384
+DEFAULT_VOCAB_CHUNK = 32768
+
+# Who computes the two plain products of the backward (dW = dZ^T X and
+# dX += dZ W, on the K-contiguous X^T / W^T / dZ^T buffers the library
+# prepares): "library" uses torch.mm / torch.addmm (hipBLASLt, fp32
+# accumulation of dX across chunks), "nmce" the library's own MFMA GEMM
+# (nmce_lmhead_ce_bwd, everything in one C call). The fused parts -- the
+# forward statistics GEMM and the recomputation of dZ -- are libnmce kernels
+# either way.
+BACKWARD_GEMM = "library"
 
 _ALIGN = 64  # hidden size granularity of the GEMM kernels
 
@@ -50,6 +59,62 @@ def _padded_hidden(t: torch.Tensor, hp: int) -> torch.Tensor:
 
 def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
+
+
+def _bwd_layout(lib, n: int, hp: int, v: int, chunk: int) -> dict:
+    import ctypes
+    buf = (ctypes.c_int64 * _lib.NMCE_LMHEAD_LAYOUT_FIELDS)()
+    _lib.check(lib.nmce_lmhead_ce_bwd_layout(n, hp, v, chunk, ctypes.addressof(buf)),
+               "nmce_lmhead_ce_bwd_layout")
+    keys = ("total", "ldt", "vpad", "chunk", "n_chunks", "off_xt", "off_wt", "off_dzt",
+            "off_dz", "off_acc")
+    return dict(zip(keys, (int(b) for b in buf)))
+
+
+def _bf16_view(ws: torch.Tensor, offset: int, rows: int, cols: int) -> torch.Tensor:
+    """A [rows, cols] bf16 view of the uint8 workspace at byte ``offset``."""
+    return ws[offset:offset + rows * cols * 2].view(torch.bfloat16).view(rows, cols)
+
+
+def _backward_library_gemm(lib, x, w, tgt, vocab_start, row_stat, go, gstride, vocab_chunk,
+                           dw):
+    """Chunked backward: libnmce recomputes dZ per vocabulary chunk; the two
+    plain products run as library GEMMs on the K-contiguous buffers (X^T, W^T,
+    dZ^T), accumulating dX in fp32 across chunks. Returns dX (bf16)."""
+    n, hp = x.shape
+    V = w.shape[0]
+    dev = x.device
+    stream = _lib.stream_handle(dev)
+    L = _bwd_layout(lib, n, hp, V, vocab_chunk)
+    ws = _workspace(L["total"], dev)
+    _launch("nmce_lmhead_ce_bwd_prepare", lib.nmce_lmhead_ce_bwd_prepare, x.data_ptr(),
+            w.data_ptr(), _lib.NMCE_BF16, n, hp, V, vocab_chunk, ws.data_ptr(), ws.numel(),
+            stream)
+    ldt, vpad, chunk = L["ldt"], L["vpad"], L["chunk"]
+    xt = _bf16_view(ws, L["off_xt"], hp, ldt)
+    wt = _bf16_view(ws, L["off_wt"], hp, vpad)
+    dzt = _bf16_view(ws, L["off_dzt"], chunk, ldt)
+    dz = _bf16_view(ws, L["off_dz"], n, chunk)
+    acc = torch.empty((n, hp), dtype=torch.float32, device=dev)
+    for c in range(L["n_chunks"]):
+        v0 = c * chunk
+        mvalid = min(chunk, V - v0)
+        mpad = (mvalid + 255) // 256 * 256
+        _launch("nmce_lmhead_ce_bwd_dz", lib.nmce_lmhead_ce_bwd_dz, x.data_ptr(), w.data_ptr(),
+                _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), vocab_start, row_stat[0].data_ptr(),
+                row_stat[1].data_ptr(), go.data_ptr(), gstride, vocab_chunk, c, ws.data_ptr(),
+                ws.numel(), stream)
+        # dW rows of this chunk: dZ^T_c [mvalid, ldt] x (X^T [hp, ldt])^T; the
+        # token padding of both operands is zero.
+        torch.mm(dzt[:mvalid], xt.t(), out=dw[v0:v0 + mvalid])
+        # dX (+)= dZ_c [n, mpad] x (W^T[:, v0:v0+mpad])^T; the vocabulary
+        # padding of both operands is zero.
+        wt_c = wt[:, v0:v0 + mpad].t()
+        if c == 0:
+            torch.mm(dz[:, :mpad], wt_c, out_dtype=torch.float32, out=acc)
+        else:
+            torch.addmm(acc, dz[:, :mpad], wt_c, out_dtype=torch.float32, out=acc)
+    return acc.to(torch.bfloat16)
 
 
 class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
@@ -133,14 +198,19 @@ class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
             if not go.is_contiguous():
                 go = go.contiguous()
             gstride = 1
-        dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
         dw = torch.empty((V, hp), dtype=torch.bfloat16, device=dev)
-        ws = _workspace(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, hp, V, ctx.vocab_chunk), dev)
-        _launch("nmce_lmhead_ce_bwd", lib.nmce_lmhead_ce_bwd, x.data_ptr(), w.data_ptr(),
-                _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), ctx.vocab_start,
-                row_stat[0].data_ptr(), row_stat[1].data_ptr(), go.data_ptr(), gstride,
-                dx.data_ptr(), dw.data_ptr(), ctx.vocab_chunk, ws.data_ptr(), ws.numel(),
-                _lib.stream_handle(dev))
+        if BACKWARD_GEMM == "nmce":
+            dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
+            ws = _workspace(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, hp, V, ctx.vocab_chunk),
+                            dev)
+            _launch("nmce_lmhead_ce_bwd", lib.nmce_lmhead_ce_bwd, x.data_ptr(), w.data_ptr(),
+                    _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), ctx.vocab_start,
+                    row_stat[0].data_ptr(), row_stat[1].data_ptr(), go.data_ptr(), gstride,
+                    dx.data_ptr(), dw.data_ptr(), ctx.vocab_chunk, ws.data_ptr(), ws.numel(),
+                    _lib.stream_handle(dev))
+        else:
+            dx = _backward_library_gemm(lib, x, w, tgt, ctx.vocab_start, row_stat, go, gstride,
+                                        ctx.vocab_chunk, dw)
         H = ctx.H
         if hp != H:
             dx = dx[:, :H]

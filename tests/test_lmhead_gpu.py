@@ -270,6 +270,32 @@ def test_fused_two_shards_combined():
     check_grad(dxs[0] + dxs[1], rdx, "dH (sum of shards)")
 
 
+@pytest.mark.parametrize("route", ["library", "nmce"])
+@pytest.mark.parametrize("chunk", [256, 768, None])
+def test_dropin_backward_routes(route, chunk):
+    """The drop-in backward through either GEMM route (library GEMMs on the
+    prepared buffers, or libnmce's own) against the fp64 closed form."""
+    import nmce
+    import nmce.lmhead as LH
+    n, h, v = 320, 128, 1900
+    x, w, t = make_inputs(n, h, v, seed=17, w_std=0.5)
+    saved = LH.BACKWARD_GEMM
+    LH.BACKWARD_GEMM = route
+    try:
+        xd = x.to(DEV).requires_grad_(True)
+        wd = w.to(DEV).requires_grad_(True)
+        loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v,
+                                                        nmce.ParallelContext.single(),
+                                                        vocab_chunk=chunk)
+        loss.backward()
+    finally:
+        LH.BACKWARD_GEMM = saved
+    rl, _, rdx, rdw = fp64_reference(x, w, t)
+    assert abs(loss.item() - rl.mean()) <= 1e-5 * abs(rl.mean())
+    check_grad(xd.grad.float().cpu().numpy(), rdx, f"dH ({route}, chunk {chunk})")
+    check_grad(wd.grad.float().cpu().numpy(), rdw, f"dW ({route}, chunk {chunk})")
+
+
 def test_fused_ragged_hidden_is_padded():
     """H = 100 is not a multiple of 64: the wrapper pads with zero columns."""
     import nmce
