@@ -21,8 +21,10 @@
 // gives each lane 16 vocabulary rows of a single token, so the per-token
 // reductions are mostly in-register, with one cross-half shuffle.
 //
-// Main loop: a 256x256 output tile per 256-lane workgroup (four waves, 2x2,
-// each 128x128 = 16 accumulators of 32x32), K in steps of 64. Operand tiles
+// Main loop: a 256x256 output tile per 512-lane workgroup (eight waves, 2x4,
+// two per SIMD, each 128x64 = 8 accumulators of 32x32), K in steps of 64.
+// Each wave reads its next fragments from LDS under the MFMAs of the current
+// ones (two register sets, one LDS read pinned after each MFMA). Operand tiles
 // move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (global_load_lds_dwordx4,
 // no VGPR staging), double-buffered, rows of 128 bytes with the 16-byte chunks
 // XOR-swizzled by ((row >> 1) & 7). gfx950's LDS has 64 banks, so a
@@ -33,7 +35,6 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include <type_traits>
 
 #include "nmce.h"
 #include "nmce_device.h"
@@ -64,15 +65,7 @@ constexpr int kFN = kWaveN / 32;       // 4 accumulators across
 constexpr int kStageA = kBM * kBK * 2;  // bytes
 constexpr int kStageB = kBN * kBK * 2;
 constexpr int kStage = kStageA + kStageB;
-#ifndef NMCE_LMHEAD_PINGPONG
-#define NMCE_LMHEAD_PINGPONG 0
-#endif
-#ifndef NMCE_LMHEAD_RING
-#define NMCE_LMHEAD_RING 4
-#endif
-// Dynamic LDS of the GEMM kernels (of the 160 KiB per CU).
-constexpr int kLdsBytes =
-    NMCE_LMHEAD_PINGPONG == 3 ? NMCE_LMHEAD_RING * (kBM + kBN) * 64 : 2 * kStage;
+constexpr int kLdsBytes = 2 * kStage;  // dynamic LDS: 128 KiB of the 160 KiB per CU
 // 1 KiB LDS blocks (8 rows x 128 B) per stage and per wave.
 constexpr int kBlocksA = kBM / 8;
 constexpr int kBlocksB = kBN / 8;
@@ -84,11 +77,7 @@ static_assert(kBlocksA % kBlocksPerWave == 0, "a wave loads blocks of one operan
 constexpr int kGroupM = NMCE_LMHEAD_GROUP_M;  // tile rows per raster group inside an XCD band
 constexpr int kXcds = 8;
 constexpr float kMaxFloorL = -1.0e38f;
-#ifndef NMCE_LMHEAD_DMA_AUX
-#define NMCE_LMHEAD_DMA_AUX 0
-#endif
-// Cache-policy bits of the direct-to-LDS operand loads.
-constexpr int kDmaAux = NMCE_LMHEAD_DMA_AUX;
+
 
 // Partial statistics cover this many vocabulary rows (one wave's rows).
 constexpr int kPartialRows = kWaveM;
@@ -122,9 +111,10 @@ __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, i
 // A rows >= M and B rows >= N are read from the last valid row (their results
 // are masked by the epilogues). Requires K % 64 == 0, lda and ldb multiples of
 // 8 elements, 16-byte aligned A and B, and 256*ld*2 < 2^32 bytes.
-__device__ __forceinline__ void gemm_mainloop_interleaved(
-    const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
-    int64_t ldb, int64_t N, int64_t K, int64_t m0, int64_t n0, char* lds, Acc& acc) {
+__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t lda,
+                                              int64_t M, const uint16_t* __restrict__ B,
+                                              int64_t ldb, int64_t N, int64_t K, int64_t m0,
+                                              int64_t n0, char* lds, Acc& acc) {
   const int lane = threadIdx.x & 63;
   // The wave index is uniform across the wave; say so, so that the load
   // bases and LDS destinations below live in scalar registers.
@@ -171,7 +161,7 @@ __device__ __forceinline__ void gemm_mainloop_interleaved(
 #pragma unroll
     for (int j = 0; j < kBlocksPerWave; ++j) {
       __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + goff[j]),
-                                       (lds_void_t*)(l + j * 1024), 16, 0, kDmaAux);
+                                       (lds_void_t*)(l + j * 1024), 16, 0, 0);
     }
   };
 
@@ -256,592 +246,6 @@ __device__ __forceinline__ void gemm_mainloop_interleaved(
   wait_vmem();
 }
 
-// Interleaved main loop with the direct-to-LDS loads of each stage spread
-// over three sub-steps instead of issued in one burst after the barrier
-// (same contract and result as gemm_mainloop_interleaved).
-__device__ __forceinline__ void gemm_mainloop_spread(
-    const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
-    int64_t ldb, int64_t N, int64_t K, int64_t m0, int64_t n0, char* lds, Acc& acc) {
-  const int lane = threadIdx.x & 63;
-  // The wave index is uniform across the wave; say so, so that the load
-  // bases and LDS destinations below live in scalar registers.
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / kWavesN, wn = wave % kWavesN;
-
-#pragma unroll
-  for (int i = 0; i < kFM; ++i)
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc.c[i][j][e] = 0.0f;
-
-  // ---- load plan: this wave fills kBlocksPerWave 1 KiB blocks per stage ----
-  // Lane p of a block writes LDS bytes [16p, 16p+16): row p/8 of the block,
-  // physical chunk p%8, which holds logical chunk (p%8) ^ ((row >> 1) & 7).
-  const int first_block = wave * kBlocksPerWave;
-  const bool load_a = first_block < kBlocksA;
-  const int row_lane = lane >> 3;
-  const char* gbase;
-  int64_t ld_op, rows_op;
-  int lds_op;
-  int blk0;
-  if (load_a) {
-    gbase = reinterpret_cast<const char*>(A + m0 * lda);
-    ld_op = lda; rows_op = M - m0; lds_op = 0; blk0 = first_block;
-  } else {
-    gbase = reinterpret_cast<const char*>(B + n0 * ldb);
-    ld_op = ldb; rows_op = N - n0; lds_op = kStageA; blk0 = first_block - kBlocksA;
-  }
-  uint32_t goff[kBlocksPerWave];
-#pragma unroll
-  for (int j = 0; j < kBlocksPerWave; ++j) {
-    const int tile_row = (blk0 + j) * 8 + row_lane;
-    const int chunk = (lane & 7) ^ ((tile_row >> 1) & 7);
-    int64_t r = tile_row;
-    if (r > rows_op - 1) r = rows_op - 1;
-    goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
-  }
-
-  // Blocks [kJ0, kJ1) of this wave's share of a stage.
-  auto issue_part = [&](int stage, int64_t k0, auto j0_c, auto j1_c) {
-    constexpr int kJ0 = decltype(j0_c)::value, kJ1 = decltype(j1_c)::value;
-    const char* g = gbase + k0 * 2;
-    char* l = lds + stage * kStage + lds_op + blk0 * 1024;
-#pragma unroll
-    for (int j = kJ0; j < kJ1; ++j) {
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + goff[j]),
-                                       (lds_void_t*)(l + j * 1024), 16, 0, kDmaAux);
-    }
-  };
-  using C0 = std::integral_constant<int, 0>;
-  using C3 = std::integral_constant<int, 3>;
-  using C6 = std::integral_constant<int, 6>;
-  using C8 = std::integral_constant<int, kBlocksPerWave>;
-  static_assert(kBlocksPerWave == 8, "the DMA spread below assumes 8 blocks per wave");
-  auto issue = [&](int stage, int64_t k0) { issue_part(stage, k0, C0{}, C8{}); };
-
-  // ---- fragment plan: 32x32x16 operands, 8 bf16 per lane -------------------
-  // A fragment fm, K sub-step s: row wm*128 + 32*fm + lane%32, logical chunk
-  // 2*s + lane/32 of that row (16 bytes).
-  const int frow = lane & 31;
-  const int fhalf = lane >> 5;
-  const int a_row_off = (wm * kWaveM + frow) * 128;
-  const int b_row_off = kStageA + (wn * kWaveN + frow) * 128;
-  int xo[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) xo[s] = (((2 * s + fhalf) ^ ((frow >> 1) & 7)) << 4);
-
-  // Fragments of one K sub-step; two sets alternate so that the LDS reads of
-  // sub-step s+1 are in flight under the 16 MFMAs of sub-step s.
-  struct Frags {
-    bf16x8_t a[kFM];
-    bf16x8_t b[kFN];
-  };
-  auto load_frags = [&](const char* st, int s, Frags& f) {
-#pragma unroll
-    for (int i = 0; i < kFM; ++i)
-      f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-      f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
-  };
-  auto mma = [&](const Frags& f) {
-#pragma unroll
-    for (int i = 0; i < kFM; ++i)
-#pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.c[i][j], 0, 0, 0);
-  };
-
-  // One sub-step of the pipeline: the LDS reads of the next fragments (8 of
-  // them) interleaved one per MFMA with the 16 MFMAs of the current ones, so
-  // that the compiler neither serialises them nor reuses registers early.
-  // One sub-step with `dma` (issuing kNDma direct-to-LDS loads) spread over
-  // its first MFMAs: MFMA, LDS read, DMA triplets.
-  auto step = [&](const char* st_next, int s_next, Frags& next, const Frags& cur, auto ndma_c,
-                  auto&& dma) {
-    constexpr int kNDma = decltype(ndma_c)::value;
-    load_frags(st_next, s_next, next);
-    mma(cur);
-    dma();
-#pragma unroll
-    for (int i = 0; i < kFM + kFN; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
-      if (i < kNDma) __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);  // 1 DMA
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, kFM * kFN - (kFM + kFN), 0);
-  };
-  auto none = []() {};
-
-  // Stage kt lives in LDS buffer kt & 1. Loads run one stage ahead: stage
-  // kt+2 is issued into buffer kt & 1 as soon as every wave has its last
-  // fragments of stage kt in registers. Past the end of K the loads repeat the
-  // last stage (in bounds, never read), which keeps the loop free of branches.
-  const int64_t kt_n = K / kBK;
-  auto k_at = [&](int64_t kt) { return (kt < kt_n ? kt : kt_n - 1) * kBK; };
-  // Stage kt+2's loads are spread: blocks 0-2 go out with the sub-step right
-  // after the barrier of stage kt, blocks 3-5 and 6-7 with the first two
-  // sub-steps of stage kt+1; they are waited for at the end of stage kt+1.
-  issue(0, 0);
-  issue_part(1, k_at(1), C0{}, C3{});
-  wait_vmem();
-  __syncthreads();
-  Frags f0, f1;
-  load_frags(lds, 0, f0);
-  using D0 = std::integral_constant<int, 0>;
-  using D2 = std::integral_constant<int, 2>;
-  using D3 = std::integral_constant<int, 3>;
-  for (int64_t kt = 0; kt + 1 < kt_n; ++kt) {
-    const char* st = lds + static_cast<int>(kt & 1) * kStage;
-    const int nb = static_cast<int>((kt + 1) & 1);
-    const int64_t kn = k_at(kt + 1);
-    step(st, 1, f1, f0, D3{}, [&]() { issue_part(nb, kn, C3{}, C6{}); });
-    step(st, 2, f0, f1, D2{}, [&]() { issue_part(nb, kn, C6{}, C8{}); });
-    step(st, 3, f1, f0, D0{}, none);
-    wait_vmem();
-    __syncthreads();
-    const int cb = static_cast<int>(kt & 1);
-    const int64_t k2 = k_at(kt + 2);
-    step(lds + nb * kStage, 0, f0, f1, D3{}, [&]() { issue_part(cb, k2, C0{}, C3{}); });
-  }
-  {
-    const char* st = lds + static_cast<int>((kt_n - 1) & 1) * kStage;
-    const int nb = static_cast<int>(kt_n & 1);
-    const int64_t kn = k_at(kt_n);
-    step(st, 1, f1, f0, D3{}, [&]() { issue_part(nb, kn, C3{}, C6{}); });
-    step(st, 2, f0, f1, D2{}, [&]() { issue_part(nb, kn, C6{}, C8{}); });
-    step(st, 3, f1, f0, D0{}, none);
-    mma(f1);
-  }
-  wait_vmem();
-}
-
-// Register-staged main loop (same contract and result as
-// gemm_mainloop_interleaved): the operand tiles move HBM/L2 -> VGPRs with
-// global_load_dwordx4 and VGPRs -> LDS with ds_write_b128 into the same
-// swizzled layout, instead of direct-to-LDS loads. The global loads of stage
-// kt+2 are issued in the middle of stage kt, right after the staged stage
-// kt+1 has been written to LDS; one barrier per stage.
-__device__ __forceinline__ void gemm_mainloop_regstage(
-    const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
-    int64_t ldb, int64_t N, int64_t K, int64_t m0, int64_t n0, char* lds, Acc& acc) {
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / kWavesN, wn = wave % kWavesN;
-
-#pragma unroll
-  for (int i = 0; i < kFM; ++i)
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc.c[i][j][e] = 0.0f;
-
-  const int first_block = wave * kBlocksPerWave;
-  const bool load_a = first_block < kBlocksA;
-  const int row_lane = lane >> 3;
-  const char* gbase;
-  int64_t ld_op, rows_op;
-  int lds_op, blk0;
-  if (load_a) {
-    gbase = reinterpret_cast<const char*>(A + m0 * lda);
-    ld_op = lda; rows_op = M - m0; lds_op = 0; blk0 = first_block;
-  } else {
-    gbase = reinterpret_cast<const char*>(B + n0 * ldb);
-    ld_op = ldb; rows_op = N - n0; lds_op = kStageA; blk0 = first_block - kBlocksA;
-  }
-  uint32_t goff[kBlocksPerWave];
-#pragma unroll
-  for (int j = 0; j < kBlocksPerWave; ++j) {
-    const int tile_row = (blk0 + j) * 8 + row_lane;
-    const int chunk = (lane & 7) ^ ((tile_row >> 1) & 7);
-    int64_t r = tile_row;
-    if (r > rows_op - 1) r = rows_op - 1;
-    goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
-  }
-  const int lds_lane = lds_op + blk0 * 1024 + lane * 16;
-  u32x4 stage_regs[kBlocksPerWave];
-  auto gload = [&](int64_t k0) {
-    const char* g = gbase + k0 * 2;
-#pragma unroll
-    for (int j = 0; j < kBlocksPerWave; ++j)
-      stage_regs[j] = *reinterpret_cast<const u32x4*>(g + goff[j]);
-  };
-  auto lwrite = [&](int buf) {
-    char* l = lds + buf * kStage + lds_lane;
-#pragma unroll
-    for (int j = 0; j < kBlocksPerWave; ++j) *reinterpret_cast<u32x4*>(l + j * 1024) = stage_regs[j];
-  };
-
-  const int frow = lane & 31;
-  const int fhalf = lane >> 5;
-  const int a_row_off = (wm * kWaveM + frow) * 128;
-  const int b_row_off = kStageA + (wn * kWaveN + frow) * 128;
-  int xo[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) xo[s] = (((2 * s + fhalf) ^ ((frow >> 1) & 7)) << 4);
-
-  struct Frags {
-    bf16x8_t a[kFM];
-    bf16x8_t b[kFN];
-  };
-  auto load_frags = [&](const char* st, int s, Frags& f) {
-#pragma unroll
-    for (int i = 0; i < kFM; ++i)
-      f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-      f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
-  };
-  auto mma = [&](const Frags& f) {
-#pragma unroll
-    for (int i = 0; i < kFM; ++i)
-#pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.c[i][j], 0, 0, 0);
-  };
-  auto step = [&](const char* st_next, int s_next, Frags& next, const Frags& cur) {
-    load_frags(st_next, s_next, next);
-    mma(cur);
-#pragma unroll
-    for (int i = 0; i < kFM + kFN; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, kFM * kFN - (kFM + kFN), 0);
-  };
-
-  const int64_t kt_n = K / kBK;
-  auto k_at = [&](int64_t kt) { return (kt < kt_n ? kt : kt_n - 1) * kBK; };
-  gload(0);
-  lwrite(0);
-  gload(k_at(1));
-  __syncthreads();
-  Frags f0, f1;
-  load_frags(lds, 0, f0);
-  for (int64_t kt = 0; kt + 1 < kt_n; ++kt) {
-    const char* st = lds + static_cast<int>(kt & 1) * kStage;
-    step(st, 1, f1, f0);
-    step(st, 2, f0, f1);
-    // Stage kt+1 -> the other buffer (its previous stage was released at the
-    // last barrier), then start stage kt+2's global loads.
-    lwrite(static_cast<int>((kt + 1) & 1));
-    gload(k_at(kt + 2));
-    step(st, 3, f1, f0);
-    __syncthreads();
-    step(lds + static_cast<int>((kt + 1) & 1) * kStage, 0, f0, f1);
-  }
-  {
-    const char* st = lds + static_cast<int>((kt_n - 1) & 1) * kStage;
-    step(st, 1, f1, f0);
-    step(st, 2, f0, f1);
-    step(st, 3, f1, f0);
-    mma(f1);
-  }
-}
-
-// Ring main loop (same contract and result as gemm_mainloop_interleaved):
-// thinner stages of K = 32 (32 KiB for both operands) in a ring of kRing
-// LDS buffers, with the direct-to-LDS loads issued kRing-1 stages ahead, so
-// that about 96 KiB per CU are in flight to cover HBM and L2 latency. Rows
-// are 64 bytes (four 16-byte chunks) with the chunks XOR-swizzled by
-// ((row >> 2) & 3): the 16 rows a ds_read_b128 serves per cycle then fall on
-// 16 distinct 16-byte bank groups of the 64 banks. One barrier per stage.
-__device__ __forceinline__ void gemm_mainloop_ring(
-    const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
-    int64_t ldb, int64_t N, int64_t K, int64_t m0, int64_t n0, char* lds, Acc& acc) {
-  constexpr int kRing = NMCE_LMHEAD_RING;
-  constexpr int kRK = 32;                            // K per stage
-  constexpr int kRowB = kRK * 2;                     // 64-byte rows
-  constexpr int kRStageA = kBM * kRowB;
-  constexpr int kRStage = (kBM + kBN) * kRowB;       // 32 KiB
-  static_assert(kRing * kRStage <= 160 * 1024, "LDS ring too large");
-  constexpr int kRBlocks = (kBM + kBN) / 16;         // 1 KiB blocks = 16 rows of 64 B
-  constexpr int kRBlocksA = kBM / 16;
-  constexpr int kRPerWave = kRBlocks / (kWavesM * kWavesN);
-  static_assert(kRBlocksA % kRPerWave == 0, "a wave loads blocks of one operand only");
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / kWavesN, wn = wave % kWavesN;
-
-#pragma unroll
-  for (int i = 0; i < kFM; ++i)
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc.c[i][j][e] = 0.0f;
-
-  // Lane p of a block writes LDS bytes [16p, 16p+16): row p/4 of the block,
-  // physical chunk p%4, which holds logical chunk (p%4) ^ ((row >> 2) & 3).
-  const int first_block = wave * kRPerWave;
-  const bool load_a = first_block < kRBlocksA;
-  const int row_lane = lane >> 2;
-  const char* gbase;
-  int64_t ld_op, rows_op;
-  int lds_op, blk0;
-  if (load_a) {
-    gbase = reinterpret_cast<const char*>(A + m0 * lda);
-    ld_op = lda; rows_op = M - m0; lds_op = 0; blk0 = first_block;
-  } else {
-    gbase = reinterpret_cast<const char*>(B + n0 * ldb);
-    ld_op = ldb; rows_op = N - n0; lds_op = kRStageA; blk0 = first_block - kRBlocksA;
-  }
-  uint32_t goff[kRPerWave];
-#pragma unroll
-  for (int j = 0; j < kRPerWave; ++j) {
-    const int tile_row = (blk0 + j) * 16 + row_lane;
-    const int chunk = (lane & 3) ^ ((tile_row >> 2) & 3);
-    int64_t r = tile_row;
-    if (r > rows_op - 1) r = rows_op - 1;
-    goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
-  }
-  const int64_t kt_n = K / kRK;
-  // Stage kt -> ring slot kt % kRing. Past the end of K the loads repeat the
-  // last stage (in bounds, never read), which keeps the vmcnt counts uniform.
-  auto issue = [&](int64_t kt) {
-    const int64_t kk = kt < kt_n ? kt : kt_n - 1;
-    const char* g = gbase + kk * kRK * 2;
-    char* l = lds + static_cast<int>(kt % kRing) * kRStage + lds_op + blk0 * 1024;
-#pragma unroll
-    for (int j = 0; j < kRPerWave; ++j)
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + goff[j]),
-                                       (lds_void_t*)(l + j * 1024), 16, 0, kDmaAux);
-  };
-  // Wait until at most `kStages` stages of this wave's loads are in flight.
-  auto wait_stages = [&](auto stages_c) {
-    constexpr int n = decltype(stages_c)::value * kRPerWave;
-    static_assert(n <= 63, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(n) : "memory");
-  };
-
-  const int frow = lane & 31;
-  const int fhalf = lane >> 5;
-  const int a_row_off = (wm * kWaveM + frow) * kRowB;
-  const int b_row_off = kRStageA + (wn * kWaveN + frow) * kRowB;
-  int xo[2];
-#pragma unroll
-  for (int s = 0; s < 2; ++s) xo[s] = (((2 * s + fhalf) ^ ((frow >> 2) & 3)) << 4);
-
-  struct Frags {
-    bf16x8_t a[kFM];
-    bf16x8_t b[kFN];
-  };
-  auto load_frags = [&](const char* st, int s, Frags& f) {
-#pragma unroll
-    for (int i = 0; i < kFM; ++i)
-      f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * kRowB + xo[s]);
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-      f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * kRowB + xo[s]);
-  };
-  auto mma = [&](const Frags& f) {
-#pragma unroll
-    for (int i = 0; i < kFM; ++i)
-#pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.c[i][j], 0, 0, 0);
-  };
-  auto step = [&](const char* st_next, int s_next, Frags& next, const Frags& cur) {
-    load_frags(st_next, s_next, next);
-    mma(cur);
-#pragma unroll
-    for (int i = 0; i < kFM + kFN; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-    }
-    __builtin_amdgcn_sched_group_barrier(0x008, kFM * kFN - (kFM + kFN), 0);
-  };
-  auto slot = [&](int64_t kt) { return lds + static_cast<int>(kt % kRing) * kRStage; };
-
-  for (int i = 0; i < kRing - 1; ++i) issue(i);
-  wait_stages(std::integral_constant<int, kRing - 2>{});  // stage 0 landed
-  __syncthreads();
-  Frags f0, f1;
-  load_frags(slot(0), 0, f0);
-  for (int64_t kt = 0; kt + 1 < kt_n; ++kt) {
-    step(slot(kt), 1, f1, f0);
-    // Stage kt+1 landed (this wave's loads; the barrier covers the others'),
-    // and every wave is done with the slot of stage kt-1, which takes stage
-    // kt+kRing-1.
-    wait_stages(std::integral_constant<int, kRing - 3>{});
-    __syncthreads();
-    issue(kt + kRing - 1);
-    step(slot(kt + 1), 0, f0, f1);
-  }
-  step(slot(kt_n - 1), 1, f1, f0);
-  mma(f1);
-  wait_stages(std::integral_constant<int, 0>{});
-}
-
-// Ping-pong main loop (same contract and result as gemm_mainloop_interleaved).
-//
-// The eight waves form two groups of four, one wave of each group per SIMD:
-// group 0 (waves 0-3) owns tile rows [0, 128), group 1 (waves 4-7) rows
-// [128, 256). Time is cut into phases separated by workgroup barriers; in
-// every phase one group runs a burst of 16 MFMAs (K = 32) from fragments
-// already in its registers while the other group reads its next fragments
-// from LDS (and group 0 also issues the DMA of a future stage), so each
-// SIMD's MFMA pipe is fed by one of its two waves at all times:
-//
-//   phase      0        1        2        3        4     ...
-//   group 0  mem(0)   mma(0)   mem(1)   mma(1)   mem(2)
-//   group 1    -      mem(0)   mma(0)   mem(1)   mma(1)
-//
-// where mem(hh) / mma(hh) are the reads / MFMAs of half-stage hh (K = 32).
-// Stage k (K = 64) lives in LDS buffer k & 1; group 0 issues its DMA in the
-// phases of its mem(2k-2) and mem(2k-1) (the buffer's previous stage was last
-// read by group 1 in the phase before) and waits for it after mma(2k-1), a
-// phase before the first read. The barriers are raw s_barrier: a wave waits
-// on its own LDS reads before each barrier and on its DMA only where stated.
-__device__ __forceinline__ void gemm_mainloop_pingpong(
-    const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
-    int64_t ldb, int64_t N, int64_t K, int64_t m0, int64_t n0, char* lds, Acc& acc) {
-  static_assert(kWavesM == 2, "ping-pong pairs the two wave rows of the tile");
-  constexpr int kDmaBlocks = (kBlocksA + kBlocksB) / (kWavesN);  // per group-0 wave per stage
-  constexpr int kDmaHalf = kDmaBlocks / 2;
-  static_assert(kBlocksA % kDmaBlocks == 0, "a wave loads blocks of one operand only");
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int wm = wave / kWavesN, wn = wave % kWavesN;
-  const bool lead = wm == 0;  // group 0: MFMAs first, issues all DMA
-
-#pragma unroll
-  for (int i = 0; i < kFM; ++i)
-#pragma unroll
-    for (int j = 0; j < kFN; ++j)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc.c[i][j][e] = 0.0f;
-
-  // DMA plan of a group-0 wave: kDmaBlocks 1 KiB blocks of one operand.
-  const int first_block = wn * kDmaBlocks;
-  const bool load_a = first_block < kBlocksA;
-  const int row_lane = lane >> 3;
-  const char* gbase;
-  int64_t ld_op, rows_op;
-  int lds_op, blk0;
-  if (load_a) {
-    gbase = reinterpret_cast<const char*>(A + m0 * lda);
-    ld_op = lda; rows_op = M - m0; lds_op = 0; blk0 = first_block;
-  } else {
-    gbase = reinterpret_cast<const char*>(B + n0 * ldb);
-    ld_op = ldb; rows_op = N - n0; lds_op = kStageA; blk0 = first_block - kBlocksA;
-  }
-  uint32_t goff[kDmaBlocks];
-#pragma unroll
-  for (int j = 0; j < kDmaBlocks; ++j) {
-    const int tile_row = (blk0 + j) * 8 + row_lane;
-    const int chunk = (lane & 7) ^ ((tile_row >> 1) & 7);
-    int64_t r = tile_row;
-    if (r > rows_op - 1) r = rows_op - 1;
-    goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
-  }
-  // Half kHalf (0/1) of stage `stage`'s DMA into buffer stage & 1.
-  auto dma = [&](int64_t stage, auto half_c) {
-    constexpr int kHalf = decltype(half_c)::value;
-    const char* g = gbase + stage * kBK * 2;
-    char* l = lds + static_cast<int>(stage & 1) * kStage + lds_op + blk0 * 1024;
-#pragma unroll
-    for (int j = 0; j < kDmaHalf; ++j) {
-      constexpr int kOff = kHalf * kDmaHalf;
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + goff[kOff + j]),
-                                       (lds_void_t*)(l + (kOff + j) * 1024), 16, 0, 0);
-    }
-  };
-  using Half0 = std::integral_constant<int, 0>;
-  using Half1 = std::integral_constant<int, 1>;
-
-  const int frow = lane & 31;
-  const int fhalf = lane >> 5;
-  const int a_row_off = (wm * kWaveM + frow) * 128;
-  const int b_row_off = kStageA + (wn * kWaveN + frow) * 128;
-  int xo[4];
-#pragma unroll
-  for (int s = 0; s < 4; ++s) xo[s] = (((2 * s + fhalf) ^ ((frow >> 1) & 7)) << 4);
-
-  struct Frags {
-    bf16x8_t a[kFM][2];
-    bf16x8_t b[kFN][2];
-  };
-  Frags f;
-  // Fragments of half kHalf of stage `stage` (K sub-steps 2*kHalf and +1).
-  auto mem = [&](int64_t stage, auto half_c) {
-    constexpr int kS0 = 2 * decltype(half_c)::value;
-    const char* st = lds + static_cast<int>(stage & 1) * kStage;
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-#pragma unroll
-      for (int i = 0; i < kFM; ++i)
-        f.a[i][q] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[kS0 + q]);
-#pragma unroll
-      for (int j = 0; j < kFN; ++j)
-        f.b[j][q] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[kS0 + q]);
-    }
-  };
-  auto mma = [&]() {
-#pragma unroll
-    for (int q = 0; q < 2; ++q)
-#pragma unroll
-      for (int i = 0; i < kFM; ++i)
-#pragma unroll
-        for (int j = 0; j < kFN; ++j)
-          acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i][q], f.b[j][q],
-                                                                acc.c[i][j], 0, 0, 0);
-  };
-  // Barrier ending a phase; the wave's own LDS reads are complete first. The
-  // scheduling fences keep every instruction (MFMAs included) in its phase.
-  auto phase_end = [&]() {
-    __builtin_amdgcn_sched_barrier(0);
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Both groups run the same straight-line sequence per half-stage,
-  //   mem(hh) [+ DMA, group 0] | barrier | mma(hh) [+ DMA wait] | barrier,
-  // group 1 one phase behind group 0 (an extra barrier first; group 0 adds
-  // one at the end), so no branch separates the accumulator updates.
-  const int64_t kt_n = K / kBK;
-  if (lead) {
-    dma(0, Half0{});
-    dma(0, Half1{});
-    wait_vmem();
-  }
-  phase_end();
-  if (!lead) phase_end();
-  for (int64_t k = 0; k < kt_n; ++k) {
-    mem(k, Half0{});
-    if (lead && k + 1 < kt_n) dma(k + 1, Half0{});
-    phase_end();
-    mma();
-    phase_end();
-    mem(k, Half1{});
-    if (lead && k + 1 < kt_n) dma(k + 1, Half1{});
-    phase_end();
-    mma();
-    __builtin_amdgcn_sched_barrier(0);
-    wait_vmem();  // group 0: stage k+1 has landed before anyone reads it
-    phase_end();
-  }
-  if (lead) phase_end();
-}
-
-__device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t lda,
-                                              int64_t M, const uint16_t* __restrict__ B,
-                                              int64_t ldb, int64_t N, int64_t K, int64_t m0,
-                                              int64_t n0, char* lds, Acc& acc) {
-#if NMCE_LMHEAD_PINGPONG == 1
-  gemm_mainloop_pingpong(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
-#elif NMCE_LMHEAD_PINGPONG == 2
-  gemm_mainloop_regstage(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
-#elif NMCE_LMHEAD_PINGPONG == 3
-  gemm_mainloop_ring(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
-#elif NMCE_LMHEAD_PINGPONG == 4
-  gemm_mainloop_spread(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
-#else
-  gemm_mainloop_interleaved(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
-#endif
-}
 
 // Row (within the wave's 128 rows) of accumulator fm, element e, for this lane:
 // the 32x32 result gives lane l column l%32 and rows 8*(e/4) + 4*(l/32) + e%4.
@@ -875,13 +279,17 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
   const int64_t vrow0 = m0 + wm * kWaveM;  // first vocabulary row of this wave
   if (vrow0 >= V) return;
   const int64_t blk = vrow0 / kPartialRows;
-  const int64_t valid_rows = V - vrow0;  // rows >= this are padding
+  // rows >= valid_rows of this wave's 128 are padding
+  const int valid_rows = static_cast<int>((V - vrow0) < kWaveM ? (V - vrow0) : kWaveM);
 #pragma unroll
   for (int fn = 0; fn < kFN; ++fn) {
     const int64_t tok = n0 + wn * kWaveN + 32 * fn + (lane & 31);
     const bool tok_ok = tok < N;
-    int64_t tl = -1;
-    if (tok_ok) tl = target[tok] - vstart - vrow0;
+    int tl = -1;  // target row within this wave's rows, or -1
+    if (tok_ok) {
+      const int64_t t = target[tok] - vstart - vrow0;
+      tl = (t >= 0 && t < kWaveM) ? static_cast<int>(t) : -1;
+    }
     float mx = kMaxFloorL;
     float pick = 0.0f;
 #pragma unroll
@@ -916,23 +324,47 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
 
 // Merge the partial statistics of nb vocabulary blocks into shard statistics:
 // max, sum exp relative to it, and the target logit (0 when not in the shard).
-__global__ __launch_bounds__(256) void lmhead_reduce_partials_kernel(
+// A workgroup takes 16 tokens; 16 slices of its threads stride over the
+// blocks with an online (max, sum) each, then merge through LDS.
+constexpr int kRedTokens = 16;
+constexpr int kRedSlices = 16;
+
+__global__ __launch_bounds__(kRedTokens * kRedSlices) void lmhead_reduce_partials_kernel(
     const float* __restrict__ pmax, const float* __restrict__ psum,
     const float* __restrict__ ptgt, int64_t nb, int64_t N, float* __restrict__ row_max,
     float* __restrict__ row_sumexp, float* __restrict__ target_logit) {
-  const int64_t t = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (t >= N) return;
-  float m = kMaxFloorL;
-  for (int64_t b = 0; b < nb; ++b) m = fmaxf(m, pmax[b * N + t]);
-  const float mc = m * kLog2e;
-  float s = 0.0f, tg = 0.0f;
-  for (int64_t b = 0; b < nb; ++b) {
-    s = fmaf(psum[b * N + t], exp2_hw(fmaf(pmax[b * N + t], kLog2e, -mc)), s);
-    tg += ptgt[b * N + t];
+  __shared__ float sm[kRedSlices][kRedTokens], ss[kRedSlices][kRedTokens],
+      st[kRedSlices][kRedTokens];
+  const int tl = threadIdx.x % kRedTokens;
+  const int slice = threadIdx.x / kRedTokens;
+  const int64_t t = static_cast<int64_t>(blockIdx.x) * kRedTokens + tl;
+  float m = kMaxFloorL, sum = 0.0f, tg = 0.0f;
+  if (t < N) {
+    for (int64_t b = slice; b < nb; b += kRedSlices) {
+      const float bm = pmax[b * N + t];
+      const float bs = psum[b * N + t];
+      tg += ptgt[b * N + t];
+      const float nm = fmaxf(m, bm);
+      sum = sum * exp2_hw((m - nm) * kLog2e) + bs * exp2_hw((bm - nm) * kLog2e);
+      m = nm;
+    }
   }
-  row_max[t] = m;
-  row_sumexp[t] = s;
-  target_logit[t] = tg;
+  sm[slice][tl] = m;
+  ss[slice][tl] = sum;
+  st[slice][tl] = tg;
+  __syncthreads();
+  if (slice == 0 && t < N) {
+    float gm = kMaxFloorL;
+    for (int k = 0; k < kRedSlices; ++k) gm = fmaxf(gm, sm[k][tl]);
+    float gs = 0.0f, gt = 0.0f;
+    for (int k = 0; k < kRedSlices; ++k) {
+      gs = fmaf(ss[k][tl], exp2_hw((sm[k][tl] - gm) * kLog2e), gs);
+      gt += st[k][tl];
+    }
+    row_max[t] = gm;
+    row_sumexp[t] = gs;
+    target_logit[t] = gt;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -962,18 +394,20 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   const int wm = wave / kWavesN, wn = wave % kWavesN;
   const int fhalf = lane >> 5;
   const int64_t vrow0 = m0 + wm * kWaveM;
-  const int64_t valid_rows = Mvalid - vrow0;
+  const int64_t vr = Mvalid - vrow0;
+  const int valid_rows = static_cast<int>(vr < 0 ? 0 : (vr < kWaveM ? vr : kWaveM));
 #pragma unroll
   for (int fn = 0; fn < kFN; ++fn) {
     const int64_t tok = n0 + wn * kWaveN + 32 * fn + (lane & 31);
     const bool tok_ok = tok < N;
     float mc = 0.0f, scale = 0.0f, g = 0.0f;
-    int64_t tl = -1;
+    int tl = -1;  // target row within this wave's rows, or -1
     if (tok_ok) {
       g = gout[tok * gout_stride];
       mc = gmax[tok] * kLog2e;
       scale = g / gsum[tok];
-      tl = target[tok] - vfirst - vrow0;
+      const int64_t t = target[tok] - vfirst - vrow0;
+      tl = (t >= 0 && t < kWaveM) ? static_cast<int>(t) : -1;
     }
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm) {
@@ -1055,15 +489,48 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
 }
 
 // bf16 transpose with zero padding: out[c * ldo + r] = in[r * ldi + c] for
-// r < R, c < C; out[c * ldo + r] = 0 for R <= r < ldo. 64x64 tiles via LDS.
+// r < R, c < C; out[c * ldo + r] = 0 for R <= r < ldo. 64x64 tiles through
+// LDS; interior tiles move 16 bytes per load and per store (ldi, ldo and the
+// base pointers 16-byte aligned), edge tiles go element by element.
 __global__ __launch_bounds__(256) void transpose_bf16_kernel(const uint16_t* __restrict__ in,
                                                              int64_t R, int64_t C, int64_t ldi,
                                                              uint16_t* __restrict__ out,
-                                                             int64_t ldo) {
-  __shared__ uint16_t t[64][65];
+                                                             int64_t ldo, int vec_ok) {
+  __shared__ uint16_t t[64][64 + 2];
   const int64_t r0 = static_cast<int64_t>(blockIdx.y) * 64;  // over ldo (padded R)
   const int64_t c0 = static_cast<int64_t>(blockIdx.x) * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int tid = threadIdx.x;
+  const bool interior = vec_ok && r0 + 64 <= R && c0 + 64 <= C && r0 + 64 <= ldo;
+  if (interior) {
+    // in: 64 rows x 8 vectors of 8 elements
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int row = tid / 8 + 32 * i;
+      const int cv = (tid % 8) * 8;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(in + (r0 + row) * ldi + c0 + cv);
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        t[row][cv + 2 * e] = static_cast<uint16_t>(w[e] & 0xffffu);
+        t[row][cv + 2 * e + 1] = static_cast<uint16_t>(w[e] >> 16);
+      }
+    }
+    __syncthreads();
+    // out: 64 rows (c) x 8 vectors of 8 elements (r)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int col = tid / 8 + 32 * i;
+      const int rv = (tid % 8) * 8;
+      uint32_t w[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = static_cast<uint32_t>(t[rv + 2 * e][col]) |
+               (static_cast<uint32_t>(t[rv + 2 * e + 1][col]) << 16);
+      *reinterpret_cast<u32x4*>(out + (c0 + col) * ldo + r0 + rv) = u32x4{w[0], w[1], w[2], w[3]};
+    }
+    return;
+  }
+  const int tx = tid & 63, ty = tid >> 6;
   for (int i = ty; i < 64; i += 4) {
     const int64_t r = r0 + i, c = c0 + tx;
     t[i][tx] = (r < R && c < C) ? in[r * ldi + c] : static_cast<uint16_t>(0);
@@ -1128,7 +595,9 @@ int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const
 int launch_transpose(const uint16_t* in, int64_t R, int64_t C, int64_t ldi, uint16_t* out,
                      int64_t ldo, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((ldo + 63) / 64));
-  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, stream, in, R, C, ldi, out, ldo);
+  const int vec_ok = aligned16(in) && aligned16(out) && ldi % 8 == 0 && ldo % 8 == 0;
+  hipLaunchKernelGGL(transpose_bf16_kernel, grid, dim3(256), 0, stream, in, R, C, ldi, out, ldo,
+                     vec_ok);
   return launch_status();
 }
 
@@ -1210,8 +679,9 @@ int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, 
                      target, vocab_start, pmax, psum, ptgt);
   if ((st = launch_status())) return st;
   hipLaunchKernelGGL(lmhead_reduce_partials_kernel,
-                     dim3(static_cast<unsigned>((n_rows + 255) / 256)), dim3(256), 0, s, pmax,
-                     psum, ptgt, nb, n_rows, row_max, row_sumexp, target_logit);
+                     dim3(static_cast<unsigned>((n_rows + kRedTokens - 1) / kRedTokens)),
+                     dim3(kRedTokens * kRedSlices), 0, s, pmax, psum, ptgt, nb, n_rows, row_max,
+                     row_sumexp, target_logit);
   return launch_status();
 }
 
