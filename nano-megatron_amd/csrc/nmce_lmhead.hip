@@ -372,7 +372,8 @@ __global__ __launch_bounds__(kRedTokens * kRedSlices) void lmhead_reduce_partial
 //   dZ[v, t] = (exp(z - gmax[t]) / gsum[t] - [v == target[t]]) * g[t]
 // (cross_entropy.py:53-65) as bf16 into dzt[v * ldt + t] and dz[t * ldz + v].
 // Rows v >= Mvalid and tokens t >= N are written as 0 (they pad the K extents
-// of the two GEMMs that follow).
+// of the two GEMMs that follow). The tile goes through LDS so that both
+// layouts leave as coalesced 16-byte stores.
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
     const uint16_t* __restrict__ Wc, const uint16_t* __restrict__ X, int64_t Mvalid,
@@ -396,9 +397,14 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   const int64_t vrow0 = m0 + wm * kWaveM;
   const int64_t vr = Mvalid - vrow0;
   const int valid_rows = static_cast<int>(vr < 0 ? 0 : (vr < kWaveM ? vr : kWaveM));
+  // The operand buffers are free once every wave is done with its last
+  // fragments; the 256x256 bf16 tile of dZ (128 KiB) is staged there.
+  __syncthreads();
+  uint32_t* P = reinterpret_cast<uint32_t*>(lds);
 #pragma unroll
   for (int fn = 0; fn < kFN; ++fn) {
-    const int64_t tok = n0 + wn * kWaveN + 32 * fn + (lane & 31);
+    const int tloc = wn * kWaveN + 32 * fn + (lane & 31);
+    const int64_t tok = n0 + tloc;
     const bool tok_ok = tok < N;
     float mc = 0.0f, scale = 0.0f, g = 0.0f;
     int tl = -1;  // target row within this wave's rows, or -1
@@ -419,26 +425,52 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
         p -= (r == tl) ? g : 0.0f;
         d[e] = (tok_ok && r < valid_rows) ? p : 0.0f;
       }
-      // dz: 4 consecutive vocabulary rows per group of 4 elements -> 8 bytes.
-      if (tok_ok) {
+      // Into the LDS tile as (even, odd) vocabulary-row pairs of one token:
+      // word P[v/2][t] = bf16(d[v]) | bf16(d[v+1]) << 16, tile-local v and t.
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int64_t v = vrow0 + 32 * fm + 8 * q + 4 * fhalf;
-          if (v < Mpad) {
-            uint2 w;
-            w.x = pack_bf16x2(d[4 * q], d[4 * q + 1]);
-            w.y = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
-            *reinterpret_cast<uint2*>(dz + tok * ldz + v) = w;
-          }
-        }
+      for (int q = 0; q < 4; ++q) {
+        const int vp = (wm * kWaveM + 32 * fm + 8 * q + 4 * fhalf) >> 1;
+        P[vp * kBN + tloc] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
+        P[(vp + 1) * kBN + tloc] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
       }
-      if (tok < ldt) {
-#pragma unroll
-        for (int e = 0; e < 16; ++e) {
-          const int64_t v = vrow0 + acc_row(fm, e, fhalf);
-          if (v < Mpad) dzt[v * ldt + tok] = f32_to_bf16(d[e]);
-        }
+    }
+  }
+  __syncthreads();
+  // dz [N, ldz]: one token row of the tile per lane (consecutive lanes take
+  // consecutive tokens, so the LDS reads are conflict-free), 8 vocabulary
+  // rows per 16-byte store.
+  {
+    const int t = threadIdx.x % kBN;
+    const int vg = threadIdx.x / kBN;  // which half of the 256 vocabulary rows
+    const int64_t tok = n0 + t;
+    if (tok < N) {
+      uint16_t* out = dz + tok * ldz + m0;
+#pragma unroll 4
+      for (int i = 0; i < kBM / 2 / 8; ++i) {
+        const int v = vg * (kBM / 2) + 8 * i;
+        const u32x4 w = {P[(v / 2) * kBN + t], P[(v / 2 + 1) * kBN + t],
+                         P[(v / 2 + 2) * kBN + t], P[(v / 2 + 3) * kBN + t]};
+        *reinterpret_cast<u32x4*>(out + v) = w;
       }
+    }
+  }
+  // dz^T [Vc, ldt]: 32 lanes cover one pair of vocabulary rows (256 tokens);
+  // each reads 8 words (8 tokens of both rows) and writes 16 bytes to each row.
+#pragma unroll 2
+  for (int it = 0; it < (kBM / 2) * (kBN / 8) / kThreads; ++it) {
+    const int lin = it * kThreads + static_cast<int>(threadIdx.x);
+    const int vp = lin / (kBN / 8);
+    const int t0 = 8 * (lin % (kBN / 8));
+    const u32x4 a = *reinterpret_cast<const u32x4*>(P + vp * kBN + t0);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(P + vp * kBN + t0 + 4);
+    const u32x4 lo = {(a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
+                      (b.x & 0xffffu) | (b.y << 16), (b.z & 0xffffu) | (b.w << 16)};
+    const u32x4 hi = {(a.x >> 16) | (a.y & 0xffff0000u), (a.z >> 16) | (a.w & 0xffff0000u),
+                      (b.x >> 16) | (b.y & 0xffff0000u), (b.z >> 16) | (b.w & 0xffff0000u)};
+    const int64_t tok0 = n0 + t0;
+    if (tok0 < ldt) {
+      *reinterpret_cast<u32x4*>(dzt + (m0 + 2 * vp) * ldt + tok0) = lo;
+      *reinterpret_cast<u32x4*>(dzt + (m0 + 2 * vp + 1) * ldt + tok0) = hi;
     }
   }
 }

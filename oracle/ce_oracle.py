@@ -24,6 +24,22 @@ Pinned by (tests/test_oracle.py):
   constant rows give log V, V = 1 gives 0;
 * planted mistakes (dropped max shift, missing mask, off-by-one offset, wrong
   sign) fail at least one of the above.
+
+The fused LM head + loss (nano_megatron/model.py:192 feeding
+cross_entropy.py:16-85):
+
+* ``lmhead_closed_form`` -- logits ``z = hidden @ weight^T`` in fp64, then
+  ``closed_form`` on them; gradients ``dhidden = dZ @ weight`` and
+  ``dweight = dZ^T @ hidden`` (the matmul backward of model.py:192).
+* ``lmhead_sharded``     -- the same over a vocabulary-sharded weight: per-rank
+  logits, ``shard_stats`` / ``combine`` / ``shard_grad`` on them, each rank's
+  weight rows and its partial hidden gradient (summed by the caller, as the
+  TP all-reduce of mappings.py:83-94 does).
+
+Pinned by (tests/test_oracle.py): fp64 autograd through
+``F.cross_entropy(hidden @ weight.T)`` (loss, both gradients), the sharded
+form summing to the full one, and planted mistakes (weight transposed into
+the hidden gradient, the onehot dropped from the weight gradient) failing.
 """
 
 from __future__ import annotations
@@ -124,3 +140,45 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
     rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
     out = rounded.astype(np.uint32).view(np.float32)
     return np.where(nan, np.float32(np.nan), out)
+
+
+def lmhead_closed_form(hidden: np.ndarray, weight: np.ndarray, target: np.ndarray,
+                       grad_output=None):
+    """Loss and gradients of ``closed_form(hidden @ weight^T)`` in fp64.
+
+    ``hidden`` [N, H], ``weight`` [V, H] (model.py:192: ``x @ self.weight.t()``),
+    ``target`` [N]. Returns ``(loss[N], dz[N, V], dhidden[N, H], dweight[V, H])``
+    where ``dz`` is the logit gradient of cross_entropy.py:53-65.
+    """
+    X = np.asarray(hidden, dtype=np.float64)
+    W = np.asarray(weight, dtype=np.float64)
+    z = X @ W.T
+    loss, dz = closed_form(z, target, grad_output)
+    return loss, dz, dz @ W, dz.T @ X
+
+
+def lmhead_sharded(hidden: np.ndarray, weight: np.ndarray, target: np.ndarray, tp: int,
+                   grad_output=None):
+    """The fused loss over ``tp`` vocabulary shards of ``weight`` (rows
+    ``[r*V/tp, (r+1)*V/tp)`` on rank r, tp_layers.py:98-110), combined the way
+    cross_entropy.py:22-45 does. Returns ``(loss[N], dhidden_parts[tp][N, H],
+    dweight[V, H])``; the ranks' hidden gradients are partial sums (the TP
+    all-reduce of the LM head's input mapping adds them)."""
+    X = np.asarray(hidden, dtype=np.float64)
+    W = np.asarray(weight, dtype=np.float64)
+    v = W.shape[0]
+    assert v % tp == 0
+    per = v // tp
+    n = X.shape[0]
+    g = np.full(n, 1.0) if grad_output is None else np.broadcast_to(
+        np.asarray(grad_output, dtype=np.float64), (n,))
+    zs = [X @ W[r * per:(r + 1) * per].T for r in range(tp)]
+    stats = [shard_stats(zs[r], target, r * per) for r in range(tp)]
+    M, S, loss = combine(stats)
+    parts, dws = [], []
+    for r in range(tp):
+        dz = shard_grad(zs[r], target, r * per, M, S, g)
+        parts.append(dz @ W[r * per:(r + 1) * per])
+        dws.append(dz.T @ X)
+    return loss, parts, np.concatenate(dws, axis=0)
+

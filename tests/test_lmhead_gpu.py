@@ -74,24 +74,15 @@ class GradRef:
         self.l1 = np.abs(ab) @ np.abs(b)
 
 
-def fp64_reference(x, w, t, vstart=0, g=None):
-    """Closed-form loss and gradients in fp64 (numpy) on the bf16 values.
-    Returns (loss, dz, GradRef for dH, GradRef for dW)."""
+def fp64_reference(x, w, t, g=None):
+    """The oracle's fp64 loss and gradients of the fused path on the bf16 values
+    (oracle/ce_oracle.py ``lmhead_closed_form``). Returns (loss, dz, GradRef
+    for dH, GradRef for dW); ``g`` defaults to the mean's 1/N."""
     X = x.double().numpy()
     W = w.double().numpy()
-    Z = X @ W.T
-    n, v = Z.shape
+    n = X.shape[0]
     g = np.full(n, 1.0 / n) if g is None else np.asarray(g, dtype=np.float64)
-    m = Z.max(axis=1, keepdims=True)
-    e = np.exp(Z - m)
-    s = e.sum(axis=1, keepdims=True)
-    tl = t.numpy() - vstart
-    own = (tl >= 0) & (tl < v)
-    zt = np.where(own, Z[np.arange(n), np.clip(tl, 0, v - 1)], 0.0)
-    loss = np.log(s[:, 0]) + m[:, 0] - zt
-    dz = e / s
-    dz[np.arange(n)[own], tl[own]] -= 1.0
-    dz *= g[:, None]
+    loss, dz, _, _ = ce_oracle.lmhead_closed_form(X, W, t.numpy(), g)
     return loss, dz, GradRef(dz, W), GradRef(dz.T.copy(), X)
 
 
@@ -337,6 +328,32 @@ def test_dropin_matches_unfused_on_stored_logits():
                GradRef(dz, w.double().numpy()), "dH vs unfused")
     check_grad(wd.grad.float().cpu().numpy(), GradRef(dz.T.copy(), x.double().numpy()),
                "dW vs unfused")
+
+
+def test_tied_embedding_and_head_gradients_sum():
+    """model.py:235-236 ties the LM head to the embedding: one parameter used by
+    the lookup and by the fused head, so its gradient is the head's dW plus the
+    embedding's scatter of dX. Checked against the oracle in fp64."""
+    import nmce
+    n, h, v = 256, 128, 1000
+    g = _gen(31)
+    w0 = (torch.randn(v, h, generator=g) * 0.5).to(torch.bfloat16)
+    ids = torch.randint(0, v, (n,), generator=g)
+    t = torch.randint(0, v, (n,), generator=g)
+    wd = w0.to(DEV).requires_grad_(True)
+    x = torch.nn.functional.embedding(ids.to(DEV), wd) * 2.0   # exact in bf16
+    loss = nmce.lmhead_vocab_parallel_cross_entropy(x, wd, t.to(DEV), 0, v,
+                                                    nmce.ParallelContext.single())
+    loss.backward()
+    X = 2.0 * w0.double().numpy()[ids.numpy()]
+    W = w0.double().numpy()
+    rl, dz, dx, dw = ce_oracle.lmhead_closed_form(X, W, t.numpy(), np.full(n, 1.0 / n))
+    ref = dw.copy()
+    np.add.at(ref, ids.numpy(), 2.0 * dx)
+    got = wd.grad.double().cpu().numpy()
+    assert abs(loss.item() - rl.mean()) <= 1e-5 * abs(rl.mean())
+    nrel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert nrel <= 8e-3, f"tied weight gradient norm-relative error {nrel:.3e}"
 
 
 def test_dropin_rejects_bad_target():

@@ -12,6 +12,10 @@ Checks, each chosen so a plausible mistake fails at least one of them:
 * planted mistakes: mutated copies of the oracle (missing target mask,
   off-by-one shard offset, combine without rescale, onehot with the wrong
   sign, a dropped max shift) must fail these checks.
+* the fused LM head + loss (``lmhead_closed_form``, ``lmhead_sharded``):
+  fp64 autograd through ``F.cross_entropy(hidden @ weight.T)`` with per-token
+  weights, the sharded form (tp 2, 4, 5) summing to it, and planted mistakes
+  (onehot missing from either gradient, shard offsets dropped) failing.
 """
 
 from __future__ import annotations
@@ -218,3 +222,81 @@ def test_planted_dropped_shift_is_caught():
     with np.errstate(over="ignore", invalid="ignore"):
         with pytest.raises(AssertionError):
             check_edge_rows(closed=_mut_closed_no_shift)
+
+
+# ------------------------------------------------ fused LM head + loss oracle
+
+def _torch_lmhead(X, W, t, g):
+    """fp64 autograd of F.cross_entropy(X @ W^T) with per-token weights g."""
+    Xt = torch.tensor(X, dtype=torch.float64, requires_grad=True)
+    Wt = torch.tensor(W, dtype=torch.float64, requires_grad=True)
+    z = Xt @ Wt.T
+    per = torch.nn.functional.cross_entropy(z, torch.tensor(t), reduction="none")
+    (per * torch.tensor(g)).sum().backward()
+    return per.detach().numpy(), Xt.grad.numpy(), Wt.grad.numpy()
+
+
+def check_lmhead(closed=O.lmhead_closed_form, sharded=O.lmhead_sharded):
+    rng = np.random.default_rng(7)
+    n, h, v = 24, 12, 40
+    X = rng.standard_normal((n, h))
+    W = rng.standard_normal((v, h)) * 0.7
+    t = rng.integers(0, v, n)
+    g = rng.uniform(0.1, 2.0, n)
+    tl, tdx, tdw = _torch_lmhead(X, W, t, g)
+    loss, dz, dx, dw = closed(X, W, t, g)
+    assert_close_rel(loss, tl, 1e-12, 1e-14, what="lmhead loss")
+    assert_close_rel(dx, tdx, 1e-10, 1e-14, what="lmhead dhidden")
+    assert_close_rel(dw, tdw, 1e-10, 1e-14, what="lmhead dweight")
+    for tp in (2, 4, 5):
+        sl, parts, sdw = sharded(X, W, t, tp, g)
+        assert_close_rel(sl, tl, 1e-12, 1e-14, what=f"lmhead tp={tp} loss")
+        assert_close_rel(sum(parts), tdx, 1e-10, 1e-14, what=f"lmhead tp={tp} dhidden")
+        assert_close_rel(sdw, tdw, 1e-10, 1e-14, what=f"lmhead tp={tp} dweight")
+
+
+def test_oracle_lmhead_against_autograd():
+    check_lmhead()
+
+
+def _lmhead_hidden_grad_without_onehot(hidden, weight, target, grad_output=None):
+    loss, dz, dx, dw = O.lmhead_closed_form(hidden, weight, target, grad_output)
+    W = np.asarray(weight, dtype=np.float64)
+    n = dz.shape[0]
+    g = np.ones(n) if grad_output is None else np.broadcast_to(grad_output, (n,))
+    # mistake: dhidden from the softmax alone (the target row of W not subtracted)
+    return loss, dz, dx + g[:, None] * W[target], dw
+
+
+def _lmhead_weight_grad_without_onehot(hidden, weight, target, grad_output=None):
+    loss, dz, dx, dw = O.lmhead_closed_form(hidden, weight, target, grad_output)
+    X = np.asarray(hidden, dtype=np.float64)
+    p = dz.copy()
+    n = p.shape[0]
+    g = np.ones(n) if grad_output is None else np.broadcast_to(grad_output, (n,))
+    p[np.arange(n), target] += g  # mistake: the onehot is not subtracted in dW
+    return loss, dz, dx, p.T @ X
+
+
+def _lmhead_shard_offset_dropped(hidden, weight, target, tp, grad_output=None):
+    X = np.asarray(hidden, dtype=np.float64)
+    W = np.asarray(weight, dtype=np.float64)
+    per = W.shape[0] // tp
+    zs = [X @ W[r * per:(r + 1) * per].T for r in range(tp)]
+    stats = [O.shard_stats(zs[r], target, 0) for r in range(tp)]  # mistake: offset 0
+    M, S, loss = O.combine(stats)
+    parts = [O.shard_grad(zs[r], target, 0, M, S, grad_output) @ W[r * per:(r + 1) * per]
+             for r in range(tp)]
+    dws = [O.shard_grad(zs[r], target, 0, M, S, grad_output).T @ X for r in range(tp)]
+    return loss, parts, np.concatenate(dws)
+
+
+@pytest.mark.parametrize("closed,sharded", [
+    (_lmhead_hidden_grad_without_onehot, O.lmhead_sharded),
+    (_lmhead_weight_grad_without_onehot, O.lmhead_sharded),
+    (O.lmhead_closed_form, _lmhead_shard_offset_dropped),
+])
+def test_planted_lmhead_mistakes_are_caught(closed, sharded):
+    with pytest.raises(AssertionError):
+        check_lmhead(closed, sharded)
+
