@@ -97,14 +97,15 @@ def parse_args():
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_ce.json"
+LMHEAD_TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_lmhead.json"
 
 
-def measured_traffic(workload: str, kernel: str):
+def measured_traffic(workload: str, kernel: str, path=TRAFFIC_FILE):
     """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE and
     WRITE_SIZE, each scaled by the same counter read on a copy of known size),
-    recorded in profiles/hbm_traffic_ce.json; None if not measured."""
+    recorded in profiles/hbm_traffic_*.json; None if not measured."""
     try:
-        doc = json.loads(TRAFFIC_FILE.read_text())
+        doc = json.loads(path.read_text())
         return doc["workloads"][workload][kernel]["bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
@@ -308,6 +309,18 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
         per_call.setdefault(cname, []).append(s_ev.elapsed_time(e_ev))
     avg_ms = {k: sum(vs) / len(vs) for k, vs in per_call.items()}
 
+    calib = None
+    if args.calibrate_copy:
+        # One nmce_stream_copy of the weight shard (known traffic) for scaling
+        # FETCH_SIZE / WRITE_SIZE read in a counter run.
+        from nmce import _lib as L
+        dst = torch.empty_like(w)
+        L.check(L.load().nmce_stream_copy(w.data_ptr(), dst.data_ptr(), w.numel() * 2,
+                                          L.stream_handle(dev)), "nmce_stream_copy")
+        torch.cuda.synchronize()
+        calib = w.numel() * 2
+        del dst
+
     gemm_flops = 2.0 * n * v * h
     dominant = "nmce_lmhead_ce_fwd_stats"
     achieved = gemm_flops / (avg_ms[dominant] * 1e-3) / 1e12
@@ -342,7 +355,7 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": None,
+            "traffic": measured_traffic(name, "lmhead_stats_kernel", LMHEAD_TRAFFIC_FILE),
             "alg_flops_per_launch": gemm_flops,
             "avg_launch_ms": avg_ms[dominant],
         },
@@ -355,6 +368,8 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
         },
         "device": torch.cuda.get_device_name(0),
     }
+    if calib is not None:
+        result["calibration_copy_bytes"] = calib
     del x, w, t, xp, wp
     torch.cuda.empty_cache()
     result["cpu_baseline"] = cpu_baseline_fused(wl, 128) if with_cpu else None
