@@ -22,11 +22,12 @@
 // reductions are mostly in-register, with one cross-half shuffle.
 //
 // Main loop: a 256x256 output tile per 512-lane workgroup (eight waves, 2x4,
-// two per SIMD, each 128x64 = 8 accumulators of 32x32), K in steps of 64.
+// two per SIMD, each 128x64 = 8 accumulators of 32x32 held in AGPRs), K in
+// steps of 64.
 // Each wave reads its next fragments from LDS under the MFMAs of the current
 // ones (two register sets, one LDS read pinned after each MFMA). Operand tiles
-// move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (global_load_lds_dwordx4,
-// no VGPR staging), double-buffered, rows of 128 bytes with the 16-byte chunks
+// move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (MUBUF buffer_load_dwordx4
+// ... lds, no VGPR staging), double-buffered, rows of 128 bytes with the 16-byte chunks
 // XOR-swizzled by ((row >> 1) & 7). gfx950's LDS has 64 banks, so a
 // ds_read_b128 serves 16 lanes (16 consecutive rows of a fragment) per cycle;
 // this swizzle puts those 16 rows on 16 distinct 16-byte bank groups (row
@@ -40,6 +41,15 @@
 #include "nmce_device.h"
 
 namespace nmce {
+
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+// MUBUF load of `size` bytes per lane straight into LDS (buffer_load_dwordx4
+// ... lds): SGPR buffer resource, per-lane byte offset, SGPR byte offset; the
+// LDS destination is the wave-uniform `lds` + 16 * lane.
+__device__ void raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) void* lds,
+                                    int size, int voffset, int soffset, int offset,
+                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
@@ -155,14 +165,23 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
     goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
   }
 
+  // Buffer resource on this wave's operand tile: base = the tile's first row,
+  // no stride, no range limit (every offset above is clamped in bounds), gfx9
+  // data format word. The K position goes in the scalar offset, so a stage's
+  // loads need no per-lane address arithmetic.
+  const uint64_t gaddr = reinterpret_cast<uint64_t>(gbase);
+  i32x4_t rsrc;
+  rsrc[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(gaddr & 0xffffffffu));
+  rsrc[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(gaddr >> 32));
+  rsrc[2] = -1;
+  rsrc[3] = 0x00020000;
   auto issue = [&](int stage, int64_t k0) {
-    const char* g = gbase + k0 * 2;
     char* l = lds + stage * kStage + lds_op + blk0 * 1024;
+    const int soff = __builtin_amdgcn_readfirstlane(static_cast<int>(k0 * 2));
 #pragma unroll
-    for (int j = 0; j < kBlocksPerWave; ++j) {
-      __builtin_amdgcn_global_load_lds(reinterpret_cast<const void*>(g + goff[j]),
-                                       (lds_void_t*)(l + j * 1024), 16, 0, 0);
-    }
+    for (int j = 0; j < kBlocksPerWave; ++j)
+      raw_buffer_load_lds(rsrc, (lds_void_t*)(l + j * 1024), 16, static_cast<int>(goff[j]), soff,
+                          0, 0);
   };
 
   // ---- fragment plan: 32x32x16 operands, 8 bf16 per lane -------------------
@@ -194,8 +213,12 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
 #pragma unroll
     for (int i = 0; i < kFM; ++i)
 #pragma unroll
-      for (int j = 0; j < kFN; ++j)
+      for (int j = 0; j < kFN; ++j) {
         acc.c[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.a[i], f.b[j], acc.c[i][j], 0, 0, 0);
+        // Keep the accumulators in AGPRs: the MFMAs then read and write them
+        // there and the arch VGPRs serve the fragment reads alone.
+        asm volatile("" : "+a"(acc.c[i][j]));
+      }
   };
 
   // One sub-step of the pipeline: the LDS reads of the next fragments (8 of
