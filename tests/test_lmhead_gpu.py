@@ -287,6 +287,64 @@ def test_dropin_backward_routes(route, chunk):
     check_grad(wd.grad.float().cpu().numpy(), rdw, f"dW ({route}, chunk {chunk})")
 
 
+def test_fused_boundary_targets_two_shards():
+    """Targets at the first and last vocabulary row of each shard and on both
+    sides of the shard boundary, TP=2 combined locally, against the oracle's
+    sharded form (cross_entropy.py:28-36 masking, tp_layers.py:98-110 offsets)."""
+    from nmce import _lib as L
+    lib = L.load()
+    n, h, v = 64, 128, 1024
+    half = v // 2
+    x, w, _ = make_inputs(n, h, v, seed=41, w_std=0.5)
+    edges = [0, half - 1, half, v - 1, 1, half + 1, half - 2, v - 2]
+    t = torch.tensor([edges[i % len(edges)] for i in range(n)], dtype=torch.int64)
+    stats = torch.stack([run_fused(x, w[r * half:(r + 1) * half].contiguous(), t, vstart=r * half,
+                                   tp_stats=True) for r in range(2)])
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    b = stats.data_ptr()
+    L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, 2, 3 * n, n, out[0].data_ptr(),
+                                out[1].data_ptr(), out[2].data_ptr(),
+                                L.stream_handle(torch.device(DEV))), "combine")
+    rl, parts, rdw = ce_oracle.lmhead_sharded(x.double().numpy(), w.double().numpy(), t.numpy(),
+                                              2, 1.0 / n)
+    np.testing.assert_allclose(out[0].cpu().numpy(), rl, rtol=1e-5, atol=1e-6)
+    # each shard's picked target logit is exactly the owned raw logit or 0
+    z = x.double().numpy() @ w.double().numpy().T
+    for r in range(2):
+        own = (t.numpy() >= r * half) & (t.numpy() < (r + 1) * half)
+        pick = stats[r, 2].cpu().numpy()
+        assert np.all(pick[~own] == 0.0)
+        np.testing.assert_allclose(pick[own], z[np.arange(n)[own], t.numpy()[own]], rtol=1e-5,
+                                   atol=1e-5)
+
+
+def test_fused_nan_propagates():
+    """A NaN hidden state gives that token a NaN loss (the reference has no
+    checks, so NaN propagates); the other tokens are unaffected."""
+    n, h, v = 64, 64, 300
+    x, w, t = make_inputs(n, h, v, seed=43, w_std=0.5)
+    x[7, 3] = float("nan")
+    loss, _, _ = run_fused(x, w, t)
+    assert np.isnan(loss[7])
+    mask = np.ones(n, dtype=bool)
+    mask[7] = False
+    rl, _, _, _ = fp64_reference(x[mask], w, t[mask])
+    np.testing.assert_allclose(loss[mask], rl, rtol=1e-5, atol=1e-6)
+
+
+def test_fused_zero_grad_output_rows():
+    """Per-token grad_output with zeros: those tokens contribute nothing to dW
+    and get a zero dH row."""
+    n, h, v = 128, 64, 500
+    x, w, t = make_inputs(n, h, v, seed=47, w_std=0.5)
+    g = np.where(np.arange(n) % 3 == 0, 0.0, 1.0 / n).astype(np.float32)
+    loss, dx, dw = run_fused(x, w, t, g=g)
+    assert np.all(dx[g == 0.0] == 0.0)
+    rl, _, rdx, rdw = fp64_reference(x, w, t, g=g.astype(np.float64))
+    check_grad(dx, rdx, "dH")
+    check_grad(dw, rdw, "dW")
+
+
 def test_fused_ragged_hidden_is_padded():
     """H = 100 is not a multiple of 64: the wrapper pads with zero columns."""
     import nmce
