@@ -760,7 +760,7 @@ int check_bwd_args(const void* hidden, const void* weight, int dtype, int64_t n_
     return NMCE_EINVAL_SHAPE;
   if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
     return NMCE_EINVAL_WORKSPACE;
-  return configure_lds();
+  return NMCE_OK;
 }
 
 int bwd_prepare(const uint16_t* X, const uint16_t* W, int64_t n_rows, int64_t H, int64_t V,
@@ -810,6 +810,7 @@ int nmce_lmhead_ce_bwd_prepare(const void* hidden, const void* weight, int dtype
   int st = check_bwd_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, vocab_chunk,
                           workspace, workspace_bytes, L);
   if (st) return st;
+  if ((st = configure_lds())) return st;
   return bwd_prepare(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight),
                      n_rows, hidden_size, vocab_local, L, static_cast<char*>(workspace),
                      static_cast<hipStream_t>(stream));
@@ -827,6 +828,7 @@ int nmce_lmhead_ce_bwd_dz(const void* hidden, const void* weight, int dtype, int
   if (st) return st;
   if (!target || !g_max || !g_sumexp || !grad_output) return NMCE_EINVAL_PTR;
   if (gout_stride < 0 || chunk_index < 0 || chunk_index >= L.n_chunks) return NMCE_EINVAL_SHAPE;
+  if ((st = configure_lds())) return st;
   return bwd_dz(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight), n_rows,
                 hidden_size, vocab_local, target, vocab_start, g_max, g_sumexp, grad_output,
                 gout_stride, chunk_index, L, static_cast<char*>(workspace),
@@ -847,6 +849,7 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
   if (!target || !g_max || !g_sumexp || !grad_output || !grad_hidden || !grad_weight)
     return NMCE_EINVAL_PTR;
   if (gout_stride < 0) return NMCE_EINVAL_SHAPE;
+  if ((st = configure_lds())) return st;
   auto s = static_cast<hipStream_t>(stream);
   char* ws = static_cast<char*>(workspace);
   const uint16_t* xt = reinterpret_cast<const uint16_t*>(ws + L.off_xt);

@@ -157,6 +157,15 @@ class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
         if not tgt.is_contiguous():
             tgt = tgt.contiguous()
 
+        ctx.vocab_start = vocab_start
+        ctx.vocab_chunk = DEFAULT_VOCAB_CHUNK if vocab_chunk is None else int(vocab_chunk)
+        ctx.hidden_shape = hidden.shape
+        ctx.H = H
+        if n == 0:  # an empty batch: nothing to launch
+            ctx.empty = True
+            ctx.weight_shape = weight.shape
+            return torch.empty(target.shape, dtype=torch.float32, device=dev)
+        ctx.empty = False
         out = torch.empty((3, n), dtype=torch.float32, device=dev)  # loss, max, sumexp
         loss, row_stat = out[0], out[1:]
         local = torch.empty((3, n), dtype=torch.float32, device=dev)
@@ -174,15 +183,16 @@ class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
                 world_size, stride, n, loss.data_ptr(), row_stat[0].data_ptr(),
                 row_stat[1].data_ptr(), stream)
 
-        ctx.vocab_start = vocab_start
-        ctx.vocab_chunk = DEFAULT_VOCAB_CHUNK if vocab_chunk is None else int(vocab_chunk)
-        ctx.hidden_shape = hidden.shape
-        ctx.H = H
         ctx.save_for_backward(x, w, tgt, row_stat)
         return loss.view(target.shape)
 
     @staticmethod
     def backward(ctx, grad_output):
+        if ctx.empty:
+            dev = grad_output.device
+            return (torch.zeros(ctx.hidden_shape, dtype=torch.bfloat16, device=dev),
+                    torch.zeros(ctx.weight_shape, dtype=torch.bfloat16, device=dev),
+                    None, None, None, None, None, None)
         x, w, tgt, row_stat = ctx.saved_tensors
         lib = _lib.load()
         dev = x.device

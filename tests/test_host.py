@@ -66,6 +66,51 @@ def test_argument_errors_before_launch(lib):
     assert lib.nmce_validate_targets(None, 4, 10, p, None) == -4
 
 
+def test_lmhead_argument_errors_before_launch(lib):
+    """The fused entry points report bad arguments before touching the device."""
+    import ctypes
+    p = 4096  # a fake, aligned device address; never dereferenced
+    ws = 1 << 40
+    fwd = lib.nmce_lmhead_ce_fwd_stats
+    assert fwd(p, p, 0, 16, 64, 100, p, 0, p, p, p, p, ws, None) == -1      # fp32 not supported
+    assert fwd(p, p, 1, 16, 100, 100, p, 0, p, p, p, p, ws, None) == -2    # H not a multiple of 64
+    assert fwd(p, p, 1, 16, 64, 0, p, 0, p, p, p, p, ws, None) == -2       # empty shard
+    assert fwd(p, p, 1, 0, 64, 100, None, 0, None, None, None, None, 0, None) == 0
+    assert fwd(p + 2, p, 1, 16, 64, 100, p, 0, p, p, p, p, ws, None) == -3
+    assert fwd(p, p, 1, 16, 64, 100, None, 0, p, p, p, p, ws, None) == -4
+    assert fwd(p, p, 1, 16, 64, 100, p, 0, p, p, p, p, 16, None) == -6     # workspace too small
+    bwd = lib.nmce_lmhead_ce_bwd_dz
+    assert bwd(p, p, 1, 16, 64, 100, p, 0, p, p, p, 0, 0, 1, p, ws, None) == -2  # chunk 1 of 1
+    assert bwd(p, p, 1, 16, 64, 100, None, 0, p, p, p, 0, 0, 0, p, ws, None) == -4
+    assert bwd(p, p, 1, 16, 64, 100, p, 0, p, p, p, -1, 0, 0, p, ws, None) == -2
+    assert lib.nmce_lmhead_ce_bwd_prepare(p, p, 1, 16, 64, 100, 0, p, 8, None) == -6
+    assert lib.nmce_lmhead_ce_bwd_layout(16, 64, 100, 0, None) == -4
+    assert lib.nmce_gemm_nt_bf16(p, 64, p, 64, 16, 16, 100, p, 0, 16, None) == -2
+    assert lib.nmce_gemm_nt_bf16(p, 64, p, 64, 16, 16, 64, p, 7, 16, None) == -1
+    assert lib.nmce_gemm_nt_bf16(p, 60, p, 64, 16, 16, 64, p, 0, 16, None) == -3
+
+
+def test_lmhead_workspace_layout(lib):
+    """The backward workspace layout at the c4 shape: padding, chunking and
+    256-byte aligned, non-overlapping regions."""
+    import ctypes
+    n, h, v, chunk = 16384, 4096, 128256, 32768
+    buf = (ctypes.c_int64 * 10)()
+    assert lib.nmce_lmhead_ce_bwd_layout(n, h, v, chunk, ctypes.addressof(buf)) == 0
+    total, ldt, vpad, ch, nch, o_xt, o_wt, o_dzt, o_dz, o_acc = list(buf)
+    assert (ldt, vpad, ch, nch) == (16384, 128256, 32768, 4)
+    regions = [(o_xt, h * ldt * 2), (o_wt, h * vpad * 2), (o_dzt, ch * ldt * 2),
+               (o_dz, n * ch * 2), (o_acc, n * h * 4)]
+    for (a, sa), (b, _) in zip(regions, regions[1:]):
+        assert a % 256 == 0 and a + sa <= b
+    assert o_acc + n * h * 4 <= total
+    assert total == lib.nmce_lmhead_ce_bwd_workspace_bytes(n, h, v, chunk)
+    # ragged sizes round up: tokens to 64, vocabulary rows to 256
+    assert lib.nmce_lmhead_ce_bwd_layout(77, 192, 513, 0, ctypes.addressof(buf)) == 0
+    assert (buf[1], buf[2], buf[3], buf[4]) == (128, 768, 768, 1)
+    assert lib.nmce_lmhead_ce_fwd_workspace_bytes(n, h, v) >= 3 * ((v + 127) // 128) * n * 4
+
+
 def test_validate_slots(lib):
     assert lib.nmce_validate_slots(0) == 0
     assert lib.nmce_validate_slots(1) == 1
@@ -82,6 +127,15 @@ def test_dropin_has_no_cpu_path():
         nmce.vocab_parallel_cross_entropy(x, t, 0, 8, nmce.ParallelContext.single())
     with pytest.raises(RuntimeError, match="no CPU path"):
         nmce._VocabParallelCrossEntropy.apply(x, t, 0, 8, None, 1)
+
+
+def test_fused_dropin_has_no_cpu_path():
+    import nmce
+    x = torch.randn(4, 64).to(torch.bfloat16)
+    w = torch.randn(10, 64).to(torch.bfloat16)
+    t = torch.zeros(4, dtype=torch.long)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        nmce._LMHeadVocabParallelCrossEntropy.apply(x, w, t, 0, 10, None, 1)
 
 
 def test_parallel_context_and_shard_rule():

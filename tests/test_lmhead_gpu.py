@@ -414,6 +414,18 @@ def test_tied_embedding_and_head_gradients_sum():
     assert nrel <= 8e-3, f"tied weight gradient norm-relative error {nrel:.3e}"
 
 
+def test_fused_empty_batch():
+    """No tokens: an empty per-token loss and zero gradients, nothing launched."""
+    import nmce
+    x = torch.zeros(0, 64, dtype=torch.bfloat16, device=DEV).requires_grad_(True)
+    w = torch.randn(100, 64, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    t = torch.zeros(0, dtype=torch.int64, device=DEV)
+    per = nmce._LMHeadVocabParallelCrossEntropy.apply(x, w, t, 0, 100, None, 1)
+    assert per.shape == (0,)
+    per.sum().backward()
+    assert x.grad.shape == (0, 64) and float(w.grad.abs().sum()) == 0.0
+
+
 def test_dropin_rejects_bad_target():
     import nmce
     x, w, t = make_inputs(64, 64, 100, seed=1)
