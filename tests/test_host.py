@@ -111,6 +111,23 @@ def test_lmhead_workspace_layout(lib):
     assert lib.nmce_lmhead_ce_fwd_workspace_bytes(n, h, v) >= 3 * ((v + 127) // 128) * n * 4
 
 
+def test_default_chunk_never_holds_full_logits(lib):
+    """With the default chunk each of the backward's two gradient buffers (dZ
+    and dZ^T of one chunk) stays under a third of the full [tokens, vocab]
+    logits at the fused workloads, and a chunk covering the shard gives the
+    one-chunk layout."""
+    import ctypes
+    from nmce import lmhead
+    buf = (ctypes.c_int64 * 10)()
+    for n, h, v in ((16384, 4096, 128256), (16384, 3072, 256000)):
+        assert lib.nmce_lmhead_ce_bwd_layout(n, h, v, lmhead.DEFAULT_VOCAB_CHUNK,
+                                             ctypes.addressof(buf)) == 0
+        chunk, n_chunks = buf[3], buf[4]
+        assert n_chunks >= 4 and 3 * chunk <= v
+        assert lib.nmce_lmhead_ce_bwd_layout(n, h, v, 1 << 20, ctypes.addressof(buf)) == 0
+        assert buf[4] == 1
+
+
 def test_validate_slots(lib):
     assert lib.nmce_validate_slots(0) == 0
     assert lib.nmce_validate_slots(1) == 1
