@@ -424,6 +424,11 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   // fragments; the 256x256 bf16 tile of dZ (128 KiB) is staged there.
   __syncthreads();
   uint32_t* P = reinterpret_cast<uint32_t*>(lds);
+  // Word (vp, t) of the tile sits at P[vp * kBN + pcol(vp, t)]: the token
+  // index is XOR-swizzled in its bits 2..5 by the block of 4 vocabulary pairs,
+  // so a column read (32 lanes, one token, 32 blocks) spreads over the banks
+  // (at most 2-way), while 4 consecutive tokens stay one aligned 16-byte group.
+  auto pcol = [](int vp, int t) { return t ^ (((vp >> 2) & 15) << 2); };
 #pragma unroll
   for (int fn = 0; fn < kFN; ++fn) {
     const int tloc = wn * kWaveN + 32 * fn + (lane & 31);
@@ -453,29 +458,25 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         const int vp = (wm * kWaveM + 32 * fm + 8 * q + 4 * fhalf) >> 1;
-        P[vp * kBN + tloc] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
-        P[(vp + 1) * kBN + tloc] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
+        // vp is even, so vp and vp + 1 share a block of 4 and a swizzle
+        const int col = pcol(vp, tloc);
+        P[vp * kBN + col] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
+        P[(vp + 1) * kBN + col] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
       }
     }
   }
   __syncthreads();
-  // dz [N, ldz]: one token row of the tile per lane (consecutive lanes take
-  // consecutive tokens, so the LDS reads are conflict-free), 8 vocabulary
-  // rows per 16-byte store.
-  {
-    const int t = threadIdx.x % kBN;
-    const int vg = threadIdx.x / kBN;  // which half of the 256 vocabulary rows
-    const int64_t tok = n0 + t;
-    if (tok < N) {
-      uint16_t* out = dz + tok * ldz + m0;
+  // dz [N, ldz]: 32 lanes per token row, each 8 consecutive vocabulary rows
+  // (16 bytes), so one store instruction writes two 512-byte row segments.
 #pragma unroll 4
-      for (int i = 0; i < kBM / 2 / 8; ++i) {
-        const int v = vg * (kBM / 2) + 8 * i;
-        const u32x4 w = {P[(v / 2) * kBN + t], P[(v / 2 + 1) * kBN + t],
-                         P[(v / 2 + 2) * kBN + t], P[(v / 2 + 3) * kBN + t]};
-        *reinterpret_cast<u32x4*>(out + v) = w;
-      }
-    }
+  for (int it = 0; it < kBN * (kBM / 8) / kThreads; ++it) {
+    const int lin = it * kThreads + static_cast<int>(threadIdx.x);
+    const int t = lin / (kBM / 8);
+    const int L = lin % (kBM / 8);  // vocabulary rows 8L .. 8L+7, pairs 4L .. 4L+3
+    const int64_t tok = n0 + t;
+    const uint32_t* col = P + 4 * L * kBN + pcol(4 * L, t);
+    const u32x4 w = {col[0], col[kBN], col[2 * kBN], col[3 * kBN]};
+    if (tok < N) *reinterpret_cast<u32x4*>(dz + tok * ldz + m0 + 8 * L) = w;
   }
   // dz^T [Vc, ldt]: 32 lanes cover one pair of vocabulary rows (256 tokens);
   // each reads 8 words (8 tokens of both rows) and writes 16 bytes to each row.
@@ -484,8 +485,8 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
     const int lin = it * kThreads + static_cast<int>(threadIdx.x);
     const int vp = lin / (kBN / 8);
     const int t0 = 8 * (lin % (kBN / 8));
-    const u32x4 a = *reinterpret_cast<const u32x4*>(P + vp * kBN + t0);
-    const u32x4 b = *reinterpret_cast<const u32x4*>(P + vp * kBN + t0 + 4);
+    const u32x4 a = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, t0));
+    const u32x4 b = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, t0 + 4));
     const u32x4 lo = {(a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
                       (b.x & 0xffffu) | (b.y << 16), (b.z & 0xffffu) | (b.w << 16)};
     const u32x4 hi = {(a.x >> 16) | (a.y & 0xffff0000u), (a.z >> 16) | (a.w & 0xffff0000u),
