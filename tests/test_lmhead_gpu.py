@@ -220,6 +220,70 @@ def test_fused_chunked_backward_matches(chunk):
     check_grad(dx1, rdx, "dH one chunk")
 
 
+def test_bwd_dz_buffers():
+    """The recomputed logit gradient itself, read back from the workspace after
+    ``nmce_lmhead_ce_bwd_dz`` for both chunks of a ragged shard (300 tokens,
+    1000 rows, chunk 512): dZ [N, chunk] against the oracle's fp64 dZ within
+    one bf16 rounding (2^-8 relative, 2^-7 where the fp32 and fp64 values
+    round to neighbours at a tie), dZ^T bit-for-bit its transpose, and the
+    padding (rows past the shard, tokens past N) exactly zero."""
+    from nmce import _lib as L
+    from nmce import lmhead as LH
+    lib = L.load()
+    n, h, v, chunk = 300, 128, 1000, 512
+    x, w, t = make_inputs(n, h, v, seed=31, x_std=1.0, w_std=0.3)
+    g = torch.rand(n, generator=_gen(32)) + 0.5
+    print(f"[dz buffers] n={n} h={h} v={v} chunk={chunk}", flush=True)
+    _, ref, _, _ = fp64_reference(x, w, t, g.double().numpy())
+    xd, wd, td = x.to(DEV), w.to(DEV), t.to(DEV)
+    stream = L.stream_handle(torch.device(DEV))
+    stats = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    fws = torch.empty(lib.nmce_lmhead_ce_fwd_workspace_bytes(n, h, v), dtype=torch.uint8,
+                      device=DEV)
+    L.check(lib.nmce_lmhead_ce_fwd_stats(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, v,
+                                         td.data_ptr(), 0, stats[0].data_ptr(),
+                                         stats[1].data_ptr(), stats[2].data_ptr(),
+                                         fws.data_ptr(), fws.numel(), stream), "fwd_stats")
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    b = stats.data_ptr()
+    L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, 1, 3 * n, n, out[0].data_ptr(),
+                                out[1].data_ptr(), out[2].data_ptr(), stream), "combine")
+    go = g.float().to(DEV)
+    lay = LH._bwd_layout(lib, n, h, v, chunk)
+    ldt = lay["ldt"]
+    assert lay["n_chunks"] == 2 and ldt == 320
+    ws = torch.zeros(lay["total"], dtype=torch.uint8, device=DEV)
+    L.check(lib.nmce_lmhead_ce_bwd_prepare(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, v,
+                                           chunk, ws.data_ptr(), ws.numel(), stream), "prepare")
+    for c in range(2):
+        # poison both gradient buffers so that every checked byte is shown written
+        ws[lay["off_dzt"]:lay["off_dzt"] + chunk * ldt * 2].fill_(0x7f)
+        ws[lay["off_dz"]:lay["off_dz"] + n * chunk * 2].fill_(0x7f)
+        L.check(lib.nmce_lmhead_ce_bwd_dz(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, v,
+                                          td.data_ptr(), 0, out[1].data_ptr(),
+                                          out[2].data_ptr(), go.data_ptr(), 1, chunk, c,
+                                          ws.data_ptr(), ws.numel(), stream), "bwd_dz")
+        torch.cuda.synchronize()
+        v0 = c * chunk
+        mvalid = min(chunk, v - v0)
+        mpad = (mvalid + 255) // 256 * 256
+        dz = LH._bf16_view(ws, lay["off_dz"], n, chunk)
+        dzt = LH._bf16_view(ws, lay["off_dzt"], chunk, ldt)
+        got = dz[:, :mvalid].double().cpu().numpy()
+        want = ref[:, v0:v0 + mvalid]
+        bound = 2.0 ** -7 * np.abs(want) + 1e-30
+        bad = np.abs(got - want) > bound
+        assert not bad.any(), (f"chunk {c}: {int(bad.sum())} dZ entries off; first at "
+                               f"{np.argwhere(bad)[0]}: {got[bad][0]} vs {want[bad][0]}")
+        assert np.abs(got - want).max() <= 2.0 ** -8 * np.abs(want).max()
+        raw = dz.view(torch.int16)
+        rawt = dzt.view(torch.int16)
+        assert torch.equal(rawt[:mvalid, :n], raw[:, :mvalid].t()), f"chunk {c}: dZ^T != dZ^T"
+        assert not raw[:, mvalid:mpad].any(), f"chunk {c}: vocabulary padding of dZ"
+        assert not rawt[mvalid:mpad, :].any(), f"chunk {c}: vocabulary padding of dZ^T"
+        assert not rawt[:, n:ldt].any(), f"chunk {c}: token padding of dZ^T"
+
+
 def test_fused_two_shards_combined():
     """TP=2 split of the vocabulary, shards combined locally: same loss and the
     same gradients (dW rows per shard, dH summed) as the full vocabulary."""
