@@ -164,12 +164,19 @@ def _exchange_stats(local: torch.Tensor, group, world_size: int) -> torch.Tensor
     """All-gather the packed ``[3, rows]`` statistics of every TP rank.
 
     One collective of 12 bytes per token instead of the reference's three
-    dependent all-reduces (cross_entropy.py:23, :38, :43).
+    dependent all-reduces (cross_entropy.py:23, :38, :43). Returns
+    ``[world_size, 3, rows]`` in rank order on ``local``'s device. A gloo group
+    gets host copies (gloo collectives are only used on CPU tensors here).
     """
-    gathered = torch.empty((world_size,) + tuple(local.shape), dtype=local.dtype,
-                           device=local.device)
-    dist.all_gather_into_tensor(gathered, local, group=group)
-    return gathered
+    host = dist.get_backend(group) == dist.Backend.GLOO and local.device.type != "cpu"
+    src = (local.cpu() if host else local).contiguous()
+    # the concatenated output form ([world * 3, rows]) is the one every
+    # backend accepts; the stacked view is the same memory
+    gathered = torch.empty((world_size * src.shape[0],) + tuple(src.shape[1:]),
+                           dtype=src.dtype, device=src.device)
+    dist.all_gather_into_tensor(gathered, src, group=group)
+    gathered = gathered.view((world_size,) + tuple(src.shape))
+    return gathered.to(local.device) if host else gathered
 
 
 class _VocabParallelCrossEntropy(torch.autograd.Function):
