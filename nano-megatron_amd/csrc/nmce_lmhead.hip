@@ -81,10 +81,11 @@ constexpr int kBlocksA = kBM / 8;
 constexpr int kBlocksB = kBN / 8;
 constexpr int kBlocksPerWave = (kBlocksA + kBlocksB) / (kWavesM * kWavesN);
 static_assert(kBlocksA % kBlocksPerWave == 0, "a wave loads blocks of one operand only");
-#ifndef NMCE_LMHEAD_GROUP_M
-#define NMCE_LMHEAD_GROUP_M 8
-#endif
-constexpr int kGroupM = NMCE_LMHEAD_GROUP_M;  // tile rows per raster group inside an XCD band
+// Tile rows per raster group inside an XCD band. The forward walks the whole
+// weight shard (hundreds of tile rows) and runs faster with groups of 4; the
+// chunked recomputation and the plain GEMM with groups of 8 (measured).
+constexpr int kGroupM = 8;
+constexpr int kGroupMStats = 4;
 constexpr int kXcds = 8;
 constexpr float kMaxFloorL = -1.0e38f;
 
@@ -100,18 +101,19 @@ __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" 
 
 // Tile index for this workgroup. The dispatcher deals workgroups to the 8 XCDs
 // round-robin (block b runs on XCD b % 8); give each XCD a contiguous band of
-// tile ids, and inside the band walk groups of kGroupM tile rows column by
+// tile ids, and inside the band walk groups of kGM tile rows column by
 // column, so the tiles that run together on one L2 share A and B stripes.
+template <int kGM>
 __device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
   const int total = tiles_m * tiles_n;
   const int b = blockIdx.x;
   const int xcd = b % kXcds;
   const int q = total / kXcds, r = total % kXcds;
   const int tid = xcd * q + (xcd < r ? xcd : r) + b / kXcds;
-  const int group = kGroupM * tiles_n;
+  const int group = kGM * tiles_n;
   const int g = tid / group;
-  const int first_m = g * kGroupM;
-  const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+  const int first_m = g * kGM;
+  const int gm = (tiles_m - first_m) < kGM ? (tiles_m - first_m) : kGM;
   const int in_g = tid - g * group;
   tm = first_m + in_g % gm;
   tn = in_g / gm;
@@ -290,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
   const int tiles_m = static_cast<int>((V + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
   int tm, tn;
-  tile_coords(tiles_m, tiles_n, tm, tn);
+  tile_coords<kGroupMStats>(tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
   gemm_mainloop(W, H, V, X, H, N, H, m0, n0, lds, acc);
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   const int tiles_m = static_cast<int>(Mpad / kBM);
   const int tiles_n = static_cast<int>((ldt + kBN - 1) / kBN);
   int tm, tn;
-  tile_coords(tiles_m, tiles_n, tm, tn);
+  tile_coords<kGroupM>(tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
   gemm_mainloop(Wc, H, Mvalid, X, H, N, H, m0, n0, lds, acc);
@@ -515,7 +517,7 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
   const int tiles_m = static_cast<int>((M + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
   int tm, tn;
-  tile_coords(tiles_m, tiles_n, tm, tn);
+  tile_coords<kGroupM>(tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
   gemm_mainloop(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
