@@ -26,13 +26,18 @@
 // steps of 64.
 // Each wave reads its next fragments from LDS under the MFMAs of the current
 // ones (two register sets, one LDS read pinned after each MFMA). Operand tiles
-// move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (MUBUF buffer_load_dwordx4
-// ... lds, no VGPR staging), double-buffered, rows of 128 bytes with the 16-byte chunks
-// XOR-swizzled by ((row >> 1) & 7). gfx950's LDS has 64 banks, so a
-// ds_read_b128 serves 16 lanes (16 consecutive rows of a fragment) per cycle;
-// this swizzle puts those 16 rows on 16 distinct 16-byte bank groups (row
-// parity picks the half of the banks, the swizzled chunk the group). Workgroups are mapped to tiles so that each XCD (one L2)
-// owns a contiguous band of tiles walked in groups that share operands.
+// move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (MUBUF
+// buffer_load_dwordx4 ... lds, no VGPR staging), double-buffered, rows of 128
+// bytes with the 16-byte chunks XOR-swizzled by ((row >> 1) & 7). gfx950's LDS
+// has 64 banks, so a ds_read_b128 serves 16 lanes (16 consecutive rows of a
+// fragment) per cycle; this swizzle puts those 16 rows on 16 distinct 16-byte
+// bank groups (row parity picks the half of the banks, the swizzled chunk the
+// group). Workgroups are mapped to tiles so that each XCD (one L2) owns a
+// contiguous band of tiles walked in groups that share operands.
+//
+// The dZ epilogue stages the bf16 tile in the freed LDS with the token index
+// XOR-swizzled by the vocabulary-pair block, so that both output layouts leave
+// as coalesced 512-byte row segments.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
