@@ -179,3 +179,13 @@ def test_product_never_imports_the_oracle():
                 continue
             for m in mods:
                 assert not m.split(".")[0] == "oracle", f"{path.name} imports {m}"
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py runs on exactly one GPU: --gpus 2 exits with status 2 and says why."""
+    import subprocess
+    import sys
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    assert "exactly one GPU" in r.stdout
