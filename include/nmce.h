@@ -127,6 +127,21 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows,
                 int64_t gout_stride, void* stream);
 
 /*
+ * nmce_ce_bwd with the upstream gradient divided by gout_div (> 0) per row:
+ * grad_output[r*gout_stride] / gout_div replaces grad_output[r*gout_stride].
+ * With gout_stride = 0 and gout_div = N this is the backward of
+ * loss.mean() (cross_entropy.py:85) folded in: the scalar gradient of the
+ * mean is read directly, and the per-token value is the same fp32 quotient
+ * torch's MeanBackward forms, so the result is bit-identical to nmce_ce_bwd
+ * on the expanded gradient. gout_div = 1 is nmce_ce_bwd.
+ */
+int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows,
+                       int64_t vocab_local, int64_t ld, int64_t ld_grad,
+                       const int64_t* target, int64_t vocab_start, const float* g_max,
+                       const float* g_sumexp, const float* grad_output,
+                       int64_t gout_stride, float gout_div, void* stream);
+
+/*
  * Measurement support (no counterpart in the reference): a plain copy of
  * `bytes` (multiple of 16, both pointers 16-byte aligned) with the loss
  * kernels' access pattern -- 16-byte non-temporal loads and stores. Its HBM

@@ -205,7 +205,8 @@ template <typename T, bool kVec, int kBlock = kBwdBlock, int kUnroll = kBwdUnrol
 __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
-    const float* __restrict__ g_sum, const float* __restrict__ gout, int64_t gstride) {
+    const float* __restrict__ g_sum, const float* __restrict__ gout, int64_t gstride,
+    float gdiv) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
   const int tid = threadIdx.x;
@@ -214,7 +215,7 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     T* gr = g + row * ldg;
     const float M = g_max[row];
     const float S = g_sum[row];
-    const float go = gout[row * gstride];
+    const float go = gout[row * gstride] / gdiv;
     const float mc = M * kLog2e;
     const float scale = go / S;
     const int64_t lt = target[row] - vstart;  // owned iff 0 <= lt < V
@@ -286,9 +287,12 @@ template <typename T, int kBlock = kFlatBlock, int kUnroll = kFlatUnroll>
 __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     const T* x, T* g, uint32_t n_vec, uint32_t vpr, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
-    const float* __restrict__ g_sum, const float* __restrict__ gout, int64_t gstride) {
+    const float* __restrict__ g_sum, const float* __restrict__ gout, int64_t gstride,
+    float gdiv) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
+  // With a broadcast gradient (the mean's) the per-row quotient is one value.
+  const float g0 = gstride == 0 ? gout[0] / gdiv : 0.0f;
   const uint32_t base = blockIdx.x * static_cast<uint32_t>(kBlock * kUnroll) + threadIdx.x;
   u32x4 v[kUnroll];
   uint32_t rows[kUnroll], cols[kUnroll];
@@ -307,7 +311,7 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     const uint32_t row = rows[u];
     const float M = g_max[row];
     const float S = g_sum[row];
-    const float go = gout[row * gstride];
+    const float go = gstride == 0 ? g0 : gout[row * gstride] / gdiv;
     const float mc = M * kLog2e;
     const float scale = go / S;
     const int64_t d = target[row] - vstart - cols[u];
@@ -455,9 +459,18 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64
                 int64_t ld, int64_t ld_grad, const int64_t* target, int64_t vocab_start,
                 const float* g_max, const float* g_sumexp, const float* grad_output,
                 int64_t gout_stride, void* stream) {
+  return nmce_ce_bwd_scaled(logits, grad, dtype, n_rows, vocab_local, ld, ld_grad, target,
+                            vocab_start, g_max, g_sumexp, grad_output, gout_stride, 1.0f, stream);
+}
+
+int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows,
+                       int64_t vocab_local, int64_t ld, int64_t ld_grad, const int64_t* target,
+                       int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                       const float* grad_output, int64_t gout_stride, float gout_div,
+                       void* stream) {
   if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
   if (n_rows < 0 || vocab_local < 1 || ld < vocab_local || ld_grad < vocab_local ||
-      gout_stride < 0)
+      gout_stride < 0 || !(gout_div > 0.0f))
     return NMCE_EINVAL_SHAPE;
   if (n_rows == 0) return NMCE_OK;
   if (!logits || !grad || !target || !g_max || !g_sumexp || !grad_output) return NMCE_EINVAL_PTR;
@@ -484,19 +497,19 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64
       hipLaunchKernelGGL((ce_bwd_flat_kernel<float>), fgrid, dim3(kFlatBlock), 0, st,
                          static_cast<const float*>(logits), static_cast<float*>(grad),
                          static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
-                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride);
+                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride, gout_div);
     else
       hipLaunchKernelGGL((ce_bwd_flat_kernel<uint16_t>), fgrid, dim3(kFlatBlock), 0, st,
                          static_cast<const uint16_t*>(logits), static_cast<uint16_t*>(grad),
                          static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
-                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride);
+                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride, gout_div);
     return launch_status();
   }
   const dim3 grid(grid_for_rows(n_rows)), block(kBwdBlock);
 #define NMCE_BWD_LAUNCH(T, V)                                                              \
   hipLaunchKernelGGL((ce_bwd_kernel<T, V>), grid, block, 0, st, static_cast<const T*>(logits), \
                      static_cast<T*>(grad), n_rows, vocab_local, ld, ld_grad, target,           \
-                     vocab_start, g_max, g_sumexp, grad_output, gout_stride)
+                     vocab_start, g_max, g_sumexp, grad_output, gout_stride, gout_div)
   if (dtype == NMCE_F32) {
     if (vec) NMCE_BWD_LAUNCH(float, true); else NMCE_BWD_LAUNCH(float, false);
   } else {

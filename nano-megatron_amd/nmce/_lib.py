@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "nmce_validate_targets": (_c_int, [_p, _i64, _i64, _p, _p]),
     "nmce_stream_copy": (_c_int, [_p, _p, _i64, _p]),
     "nmce_ce_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _p]),
+    "nmce_ce_bwd_scaled": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64,
+                                    ctypes.c_float, _p]),
     "nmce_lmhead_ce_fwd_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "nmce_lmhead_ce_fwd_stats": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p,
                                           _p, _i64, _p]),

@@ -179,6 +179,98 @@ def _exchange_stats(local: torch.Tensor, group, world_size: int) -> torch.Tensor
     return gathered.to(local.device) if host else gathered
 
 
+def _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace):
+    """Forward of one shard (cross_entropy.py:17-50): returns the flat per-token
+    fp32 loss and leaves on ``ctx`` what the backward needs."""
+    _check_inputs(logits, target, vocab_start, vocab_end)
+    lib = _lib.load()
+    dev = logits.device
+    stream = _lib.stream_handle(dev)
+    V = logits.shape[-1]
+
+    rows = _as_rows(logits)
+    if inplace is None:
+        inplace = logits.grad_fn is not None
+    elif inplace and logits.grad_fn is None and logits.requires_grad:
+        raise ValueError("nmce: refusing to write the gradient into a leaf tensor; "
+                         "pass inplace=False or None")
+    if rows is None:  # not viewable as [rows, V]: work on a contiguous copy
+        rows = logits.contiguous().view(-1, V)
+        inplace = False
+    n = rows.shape[0]
+    ld = rows.stride(0) if n > 1 else V
+    tgt = target.reshape(-1)
+    if not tgt.is_contiguous():
+        tgt = tgt.contiguous()
+
+    dcode = _lib.dtype_code(rows.dtype)
+    # out[0] = per-token loss, out[1] = global row max, out[2] = global exp-sum
+    out = torch.empty((3, n), dtype=torch.float32, device=dev)
+    loss, row_stat = out[0], out[1:]
+    if world_size == 1:
+        # One shard holds the whole vocabulary: statistics and loss in one pass.
+        _launch("nmce_ce_fwd", lib.nmce_ce_fwd, rows.data_ptr(), dcode, n, V, ld,
+                tgt.data_ptr(), loss.data_ptr(), row_stat[0].data_ptr(),
+                row_stat[1].data_ptr(), stream)
+    else:
+        local = torch.empty((3, n), dtype=torch.float32, device=dev)
+        _launch("nmce_ce_fwd_stats", lib.nmce_ce_fwd_stats, rows.data_ptr(), dcode, n, V, ld,
+                tgt.data_ptr(), vocab_start, local[0].data_ptr(), local[1].data_ptr(),
+                local[2].data_ptr(), stream)
+        stats = _exchange_stats(local, group, world_size)
+        _launch("nmce_ce_combine", lib.nmce_ce_combine, stats.data_ptr(),
+                stats.data_ptr() + 4 * n, stats.data_ptr() + 8 * n, world_size, 3 * n, n,
+                loss.data_ptr(), row_stat[0].data_ptr(), row_stat[1].data_ptr(), stream)
+
+    ctx.inplace = bool(inplace)
+    ctx.vocab_start = vocab_start
+    ctx.logits_shape = logits.shape
+    ctx.ld = ld
+    # `rows` aliases `logits` unless a contiguous copy was made above.
+    ctx.save_for_backward(rows, tgt, row_stat, logits if ctx.inplace else None)
+    return loss
+
+
+def _grad_operand(grad_output):
+    """(fp32 tensor, row stride) for the kernels; stride 0 for an expanded
+    scalar such as the gradient torch's MeanBackward passes."""
+    go = grad_output
+    if go.dtype != torch.float32:
+        go = go.float()
+    if go.numel() > 0 and all(s == 0 for s in go.stride()):
+        return go, 0
+    go = go.reshape(-1)
+    if not go.is_contiguous():
+        go = go.contiguous()
+    return go, 1
+
+
+def _ce_backward(ctx, go, gstride, gdiv):
+    """Backward of one shard (cross_entropy.py:53-65) with the per-token
+    gradient ``go[r * gstride] / gdiv``; returns the logits gradient."""
+    rows, tgt, row_stat, original = ctx.saved_tensors
+    lib = _lib.load()
+    n, V = rows.shape
+    if ctx.inplace:
+        out = rows
+        ld_out = ctx.ld
+    else:
+        out = torch.empty((n, V), dtype=rows.dtype, device=rows.device)
+        ld_out = V
+    _launch("nmce_ce_bwd_scaled", lib.nmce_ce_bwd_scaled,
+            rows.data_ptr(), out.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, ld_out,
+            tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
+            go.data_ptr(), gstride, gdiv, _lib.stream_handle(rows.device))
+    if ctx.inplace:
+        # The logits now hold the gradient: make later readers that saved
+        # them fail their version check.
+        torch.autograd.graph.increment_version(original)
+        grad = original.detach()
+    else:
+        grad = out.view(ctx.logits_shape)
+    return grad
+
+
 class _VocabParallelCrossEntropy(torch.autograd.Function):
     """Per-token loss over a vocabulary shard (cross_entropy.py:16-65).
 
@@ -189,86 +281,38 @@ class _VocabParallelCrossEntropy(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None):
-        _check_inputs(logits, target, vocab_start, vocab_end)
-        lib = _lib.load()
-        dev = logits.device
-        stream = _lib.stream_handle(dev)
-        V = logits.shape[-1]
-
-        rows = _as_rows(logits)
-        if inplace is None:
-            inplace = logits.grad_fn is not None
-        elif inplace and logits.grad_fn is None and logits.requires_grad:
-            raise ValueError("nmce: refusing to write the gradient into a leaf tensor; "
-                             "pass inplace=False or None")
-        if rows is None:  # not viewable as [rows, V]: work on a contiguous copy
-            rows = logits.contiguous().view(-1, V)
-            inplace = False
-        n = rows.shape[0]
-        ld = rows.stride(0) if n > 1 else V
-        tgt = target.reshape(-1)
-        if not tgt.is_contiguous():
-            tgt = tgt.contiguous()
-
-        dcode = _lib.dtype_code(rows.dtype)
-        # out[0] = per-token loss, out[1] = global row max, out[2] = global exp-sum
-        out = torch.empty((3, n), dtype=torch.float32, device=dev)
-        loss, row_stat = out[0], out[1:]
-        if world_size == 1:
-            # One shard holds the whole vocabulary: statistics and loss in one pass.
-            _launch("nmce_ce_fwd", lib.nmce_ce_fwd, rows.data_ptr(), dcode, n, V, ld,
-                    tgt.data_ptr(), loss.data_ptr(), row_stat[0].data_ptr(),
-                    row_stat[1].data_ptr(), stream)
-        else:
-            local = torch.empty((3, n), dtype=torch.float32, device=dev)
-            _launch("nmce_ce_fwd_stats", lib.nmce_ce_fwd_stats, rows.data_ptr(), dcode, n, V, ld,
-                    tgt.data_ptr(), vocab_start, local[0].data_ptr(), local[1].data_ptr(),
-                    local[2].data_ptr(), stream)
-            stats = _exchange_stats(local, group, world_size)
-            _launch("nmce_ce_combine", lib.nmce_ce_combine, stats.data_ptr(),
-                    stats.data_ptr() + 4 * n, stats.data_ptr() + 8 * n, world_size, 3 * n, n,
-                    loss.data_ptr(), row_stat[0].data_ptr(), row_stat[1].data_ptr(), stream)
-
-        ctx.inplace = bool(inplace)
-        ctx.vocab_start = vocab_start
-        ctx.logits_shape = logits.shape
-        ctx.ld = ld
-        # `rows` aliases `logits` unless a contiguous copy was made above.
-        ctx.save_for_backward(rows, tgt, row_stat, logits if ctx.inplace else None)
+        loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
+                           inplace)
         return loss.view(target.shape)
 
     @staticmethod
     def backward(ctx, grad_output):
-        rows, tgt, row_stat, original = ctx.saved_tensors
-        lib = _lib.load()
-        n, V = rows.shape
-        go = grad_output
+        go, gstride = _grad_operand(grad_output)
+        return _ce_backward(ctx, go, gstride, 1.0), None, None, None, None, None, None
+
+
+class _VocabParallelCrossEntropyMean(torch.autograd.Function):
+    """``_VocabParallelCrossEntropy`` followed by ``.mean()`` (cross_entropy.py:85)
+    as one node: the forward returns the 0-dim mean (torch's, on the same
+    per-token values), and the backward hands the scalar gradient of the mean
+    straight to the kernel, which divides it by the token count per row.
+    That is the same fp32 quotient torch's MeanBackward would expand, so the
+    gradient is bit-identical, without MeanBackward's two kernels.
+    """
+
+    @staticmethod
+    def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None):
+        loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
+                           inplace)
+        ctx.n_tokens = loss.numel()
+        return loss.mean()
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        go = grad_output.reshape(1)
         if go.dtype != torch.float32:
             go = go.float()
-        if go.numel() > 0 and all(s == 0 for s in go.stride()):
-            gstride = 0  # expanded scalar, e.g. from loss.mean()
-        else:
-            go = go.reshape(-1)
-            if not go.is_contiguous():
-                go = go.contiguous()
-            gstride = 1
-        if ctx.inplace:
-            out = rows
-            ld_out = ctx.ld
-        else:
-            out = torch.empty((n, V), dtype=rows.dtype, device=rows.device)
-            ld_out = V
-        _launch("nmce_ce_bwd", lib.nmce_ce_bwd,
-                rows.data_ptr(), out.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, ld_out,
-                tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
-                go.data_ptr(), gstride, _lib.stream_handle(rows.device))
-        if ctx.inplace:
-            # The logits now hold the gradient: make later readers that saved
-            # them fail their version check.
-            torch.autograd.graph.increment_version(original)
-            grad = original.detach()
-        else:
-            grad = out.view(ctx.logits_shape)
+        grad = _ce_backward(ctx, go, 0, float(max(ctx.n_tokens, 1)))
         return grad, None, None, None, None, None, None
 
 
@@ -295,8 +339,8 @@ def vocab_parallel_cross_entropy(
     # The loss kernels are enqueued before the host waits for the check, so
     # the GPU is busy while the host reads the counts. They never read out of
     # bounds on a bad target; their result is discarded when the check fails.
-    loss = _VocabParallelCrossEntropy.apply(
+    loss = _VocabParallelCrossEntropyMean.apply(
         logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace)
     if pending is not None:
         pending.raise_if_bad()
-    return loss.mean()
+    return loss

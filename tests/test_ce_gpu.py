@@ -488,3 +488,33 @@ def test_stream_copy_calibration_kernel():
     torch.cuda.synchronize()
     assert torch.equal(src, dst)
     assert lib.nmce_stream_copy(src.data_ptr(), dst.data_ptr(), 12, None) == -2
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_wrapper_mean_backward_is_bit_identical(dtype, inplace):
+    """The wrapper folds loss.mean() (cross_entropy.py:85) into the kernel: its
+    gradient must equal, bit for bit, the per-token Function followed by
+    torch's .mean() and MeanBackward, and its loss must be torch's mean."""
+    import nmce
+    print(f"[gpu] wrapper mean {dtype} inplace={inplace}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    b, s, v = 3, 37, 1000
+    base = (torch.randn(b, s, v, device=DEV, generator=g) * 3.0).to(dtype)
+    t = torch.randint(0, v, (b, s), device=DEV, generator=g)
+    ctx = nmce.ParallelContext.single()
+    results = []
+    for fused_mean in (True, False):
+        leaf = base.detach().clone().requires_grad_(True)
+        logits = leaf * 1.0 if inplace else leaf
+        if fused_mean:
+            loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, inplace=inplace)
+        else:
+            loss = nmce._VocabParallelCrossEntropy.apply(logits, t, 0, v, None, 1,
+                                                         inplace).mean()
+        (loss * 0.37).backward()
+        results.append((loss.detach().clone(), leaf.grad.detach().clone()))
+    (l1, g1), (l2, g2) = results
+    assert torch.equal(l1, l2), (l1.item(), l2.item())
+    assert torch.equal(g1.view(torch.int16) if dtype == torch.bfloat16 else g1,
+                       g2.view(torch.int16) if dtype == torch.bfloat16 else g2)

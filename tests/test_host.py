@@ -62,6 +62,9 @@ def test_argument_errors_before_launch(lib):
     assert lib.nmce_ce_bwd(p, p, 1, 4, 8, 8, 8, p, 0, p, p, p, -1, None) == -2
     assert lib.nmce_ce_bwd(p, p, 2, 4, 8, 8, 8, p, 0, p, p, p, 0, None) == -1
     assert lib.nmce_ce_bwd(p, p + 1, 1, 4, 8, 8, 8, p, 0, p, p, p, 0, None) == -3
+    assert lib.nmce_ce_bwd_scaled(p, p, 1, 4, 8, 8, 8, p, 0, p, p, p, 0, 0.0, None) == -2
+    assert lib.nmce_ce_bwd_scaled(p, p, 1, 4, 8, 8, 8, p, 0, p, p, p, 0, -1.0, None) == -2
+    assert lib.nmce_ce_bwd_scaled(p, p, 1, 0, 8, 8, 8, None, 0, None, None, None, 0, 2.0, None) == 0
     assert lib.nmce_validate_targets(p, 4, 0, p, None) == -2
     assert lib.nmce_validate_targets(None, 4, 10, p, None) == -4
 
