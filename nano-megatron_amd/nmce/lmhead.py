@@ -30,6 +30,13 @@ import torch
 
 from . import _lib
 from .cross_entropy import _check_target, _exchange_stats, _launch, launch_target_check
+from .mappings import (
+    copy_to_tensor_parallel_region,
+    gather_from_sequence_parallel_region,
+    gather_tokens_rank_major,
+    targets_rank_major,
+)
+from .parallel import divide
 
 # Default vocabulary rows per backward chunk: the chunk's logit gradient is
 # held twice in bf16 (4 * tokens * chunk bytes), so no tensor the size of the
@@ -260,10 +267,28 @@ def lmhead_vocab_parallel_cross_entropy(
     Equals ``vocab_parallel_cross_entropy(hidden @ weight.t(), target,
     vocab_start, vocab_end, ctx)`` (cross_entropy.py:68-85 after
     model.py:192) without storing the logits. ``hidden`` is ``[b, s, H]`` (or
-    ``[tokens, H]``), ``weight`` is ``[V/tp, H]``, both bf16; returns a 0-dim
-    fp32 tensor. Same ``ValueError`` as the reference for an out-of-range
-    target.
+    ``[tokens, H]``), ``weight`` is ``[V/tp, H]``; returns a 0-dim fp32
+    tensor. Same ``ValueError`` as the reference for an out-of-range target.
+
+    The product is computed in bf16. Inside a bf16 autocast region (as
+    model.py:255-257 runs the LM head) an fp32 ``hidden`` or ``weight`` is cast
+    to bf16 the way autocast casts a matmul's operands: through autograd, so an
+    fp32 parameter receives the bf16 gradient cast back to fp32 and summed into
+    its ``.grad`` with every other use of it (the tied embedding,
+    model.py:235-236). Outside autocast, both must already be bf16.
     """
+    if not (hidden.is_cuda and weight.is_cuda):
+        raise RuntimeError("nmce: hidden and weight must be on a ROCm device "
+                           "(there is no CPU path)")
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        dev_type = hidden.device.type
+        if not (torch.is_autocast_enabled(dev_type)
+                and torch.get_autocast_dtype(dev_type) == torch.bfloat16):
+            raise TypeError("nmce: the fused LM head computes in bf16; got hidden "
+                            f"{hidden.dtype}, weight {weight.dtype} outside a bf16 autocast "
+                            "region")
+        hidden = hidden.to(torch.bfloat16)
+        weight = weight.to(torch.bfloat16)
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
     _check_target(target, hidden.shape[:-1], hidden.device)
     pending = launch_target_check(target, vocab_size) if validate else None
@@ -272,3 +297,57 @@ def lmhead_vocab_parallel_cross_entropy(
     if pending is not None:
         pending.raise_if_bad()
     return loss.mean()
+
+
+class FusedParallelLMHead(torch.nn.Module):
+    """Vocabulary-sharded output projection with the loss fused in.
+
+    Drop-in for nano_megatron's ``ParallelLMHead`` (model.py:169-192): the
+    same constructor ``(config, ctx)`` (reads ``config.vocab_size``,
+    ``config.n_embd`` and ``config.sequence_parallel``), the same ``weight``
+    parameter ``[V/tp, n_embd]`` initialised N(0, 0.02^2) and marked
+    ``tensor_parallel_sharded``, so ``lm_head.weight = embedding.weight`` ties
+    it as model.py:235-236 does. ``forward(x)`` returns the logits exactly as
+    the reference's forward does (a plain matmul; there is nothing to fuse).
+    ``forward(x, labels)`` returns the mean cross entropy of those logits
+    against the full-vocabulary ``labels`` ``[B, S]`` without storing them,
+    i.e. what ``vocab_parallel_cross_entropy(self(x), labels, *range, ctx)``
+    returns (model.py:277-281).
+
+    The input mapping is the reference's (model.py:188-191): ``f`` (identity,
+    all-reduced input gradient) at TP > 1, or the sequence all-gather under
+    sequence parallelism, which the loss takes in rank-major token order (no
+    transposes; the labels are permuted to match).
+    """
+
+    def __init__(self, config, ctx):
+        super().__init__()
+        self.ctx = ctx
+        per_partition = divide(config.vocab_size, ctx.tp_size)
+        self.weight = torch.nn.Parameter(torch.empty(per_partition, config.n_embd))
+        self.weight.tensor_parallel_sharded = True
+        self.sequence_parallel = bool(getattr(config, "sequence_parallel", False))
+        self.vocab_chunk = None  # backward chunk; None = DEFAULT_VOCAB_CHUNK
+        torch.nn.init.normal_(self.weight, std=0.02)
+
+    def vocab_range(self) -> tuple[int, int]:
+        """This rank's global id range (model.py:242-245)."""
+        per = self.weight.shape[0]
+        return self.ctx.tp_rank * per, (self.ctx.tp_rank + 1) * per
+
+    def forward(self, x: torch.Tensor, labels: torch.Tensor | None = None) -> torch.Tensor:
+        if labels is None:
+            if self.sequence_parallel:
+                x = gather_from_sequence_parallel_region(x, self.ctx)
+            else:
+                x = copy_to_tensor_parallel_region(x, self.ctx)
+            return x @ self.weight.t()
+        start, end = self.vocab_range()
+        if self.sequence_parallel:
+            rows = gather_tokens_rank_major(x, self.ctx)
+            target = targets_rank_major(labels, self.ctx.tp_size)
+        else:
+            rows = copy_to_tensor_parallel_region(x, self.ctx)
+            target = labels
+        return lmhead_vocab_parallel_cross_entropy(rows, self.weight, target, start, end,
+                                                   self.ctx, vocab_chunk=self.vocab_chunk)

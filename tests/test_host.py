@@ -158,6 +158,31 @@ def test_fused_dropin_has_no_cpu_path():
         nmce._LMHeadVocabParallelCrossEntropy.apply(x, w, t, 0, 10, None, 1)
 
 
+def test_fused_lm_head_module_mirrors_parallel_lm_head():
+    """FusedParallelLMHead(config, ctx) has ParallelLMHead's weight layout,
+    initialisation and attributes (model.py:169-192); its logits path is the
+    reference's plain product; the fused loss has no CPU path."""
+    import types
+    import nmce
+    cfg = types.SimpleNamespace(vocab_size=1000, n_embd=64, sequence_parallel=False)
+    torch.manual_seed(0)
+    head = nmce.FusedParallelLMHead(cfg, nmce.ParallelContext.single())
+    assert head.weight.shape == (1000, 64) and head.weight.dtype == torch.float32
+    assert head.weight.tensor_parallel_sharded is True
+    assert abs(float(head.weight.std()) - 0.02) < 2e-3
+    assert head.vocab_range() == (0, 1000)
+    x = torch.randn(2, 3, 64)
+    assert torch.equal(head(x), x @ head.weight.t())
+    labels = torch.zeros(2, 3, dtype=torch.long)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        head(x, labels)
+    tp2 = nmce.ParallelContext(rank=1, world_size=2, tp_size=2, tp_rank=1, pp_size=1,
+                               pp_rank=0, dp_size=1, dp_rank=0)
+    assert nmce.FusedParallelLMHead(cfg, tp2).vocab_range() == (500, 1000)
+    with pytest.raises(ValueError, match="not divisible"):
+        nmce.FusedParallelLMHead(types.SimpleNamespace(vocab_size=1001, n_embd=8), tp2)
+
+
 def test_parallel_context_and_shard_rule():
     import nmce
     ctx = nmce.ParallelContext.single()

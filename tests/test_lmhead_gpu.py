@@ -478,6 +478,50 @@ def test_tied_embedding_and_head_gradients_sum():
     assert nrel <= 8e-3, f"tied weight gradient norm-relative error {nrel:.3e}"
 
 
+def test_fused_head_module_fp32_tied_weight_under_autocast():
+    """GPT.forward's tail with the fused head (model.py:235-236, 255-281): an
+    fp32 parameter shared by the embedding lookup and FusedParallelLMHead, run
+    under bf16 autocast. The head consumes the parameter rounded to bf16 (as
+    autocast's matmul does), and the parameter's fp32 .grad is the head's dW
+    plus the lookup's scatter of dX, against the oracle in fp64. The logits
+    path is autocast's own product, and outside autocast the fp32 weight is
+    refused."""
+    import types
+    import nmce
+    b, s, h, v = 2, 128, 128, 1000
+    cfg = types.SimpleNamespace(vocab_size=v, n_embd=h, sequence_parallel=False)
+    torch.manual_seed(41)
+    head = nmce.FusedParallelLMHead(cfg, nmce.ParallelContext.single())
+    with torch.no_grad():
+        head.weight.mul_(25.0)  # std 0.5: a loss well away from log V
+    head = head.to(DEV)
+    W = head.weight
+    g = _gen(41)
+    ids = torch.randint(0, v, (b, s), generator=g)
+    t = torch.randint(0, v, (b, s), generator=g)
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        x = torch.nn.functional.embedding(ids.to(DEV), W).to(torch.bfloat16) * 2.0
+        loss = head(x, t.to(DEV))
+        logits = head(x)
+        want_logits = x @ W.t()
+    loss.backward()
+    assert W.grad.dtype == torch.float32 and logits.dtype == torch.bfloat16
+    assert torch.equal(logits, want_logits)
+    n = b * s
+    Wb = W.detach().to(torch.bfloat16).double().cpu().numpy()
+    X = 2.0 * Wb[ids.reshape(-1).numpy()]
+    rl, _, dx, dw = ce_oracle.lmhead_closed_form(X, Wb, t.reshape(-1).numpy(),
+                                                 np.full(n, 1.0 / n))
+    ref = dw.copy()
+    np.add.at(ref, ids.reshape(-1).numpy(), 2.0 * dx)
+    assert abs(loss.item() - rl.mean()) <= 1e-5 * abs(rl.mean())
+    got = W.grad.double().cpu().numpy()
+    nrel = np.linalg.norm(got - ref) / np.linalg.norm(ref)
+    assert nrel <= 8e-3, f"tied fp32 weight gradient norm-relative error {nrel:.3e}"
+    with pytest.raises(TypeError, match="bf16"):
+        head(x.detach(), t.to(DEV))
+
+
 def test_fused_empty_batch():
     """No tokens: an empty per-token loss and zero gradients, nothing launched."""
     import nmce
