@@ -315,10 +315,12 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
   for (int fn = 0; fn < kFN; ++fn) {
     const int64_t tok = n0 + wn * kWaveN + 32 * fn + (lane & 31);
     const bool tok_ok = tok < N;
-    int tl = -1;  // target row within this wave's rows, or -1
+    int tl = -1;  // target row within this wave's valid rows, or -1
     if (tok_ok) {
+      // Rows past the shard's end pad the last block (they repeat its last
+      // row); a target there belongs to the next shard and picks nothing here.
       const int64_t t = target[tok] - vstart - vrow0;
-      tl = (t >= 0 && t < kWaveM) ? static_cast<int>(t) : -1;
+      tl = (t >= 0 && t < valid_rows) ? static_cast<int>(t) : -1;
     }
     float mx = kMaxFloorL;
     float pick = 0.0f;
@@ -448,7 +450,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
       mc = gmax[tok] * kLog2e;
       scale = g / gsum[tok];
       const int64_t t = target[tok] - vfirst - vrow0;
-      tl = (t >= 0 && t < kWaveM) ? static_cast<int>(t) : -1;
+      tl = (t >= 0 && t < valid_rows) ? static_cast<int>(t) : -1;
     }
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm) {

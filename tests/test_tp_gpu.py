@@ -1,18 +1,19 @@
-"""Tensor parallelism end to end on one GPU: two ranks share cuda:0 and talk
-over gloo (host copies), so every TP > 1 code path of the drop-ins runs on
-the HIP kernels.
+"""Tensor parallelism end to end on one GPU: two or four ranks (the reference's
+own TP checks use tp 2 and 4, check_tp_math.py:94-134) share cuda:0 and talk
+over gloo (host copies), so every TP > 1 code path of the drop-ins runs on the
+HIP kernels.
 
-* unfused (cross_entropy.py:16-85 at world_size 2): each rank holds a
-  ``[B, S, V/2]`` shard of bf16 logits; the packed statistics are all-gathered
+* unfused (cross_entropy.py:16-85 at world_size tp): each rank holds a
+  ``[B, S, V/tp]`` shard of bf16 logits; the packed statistics are all-gathered
   once and combined on each rank;
 * fused, TP without sequence parallelism (model.py:188-192 with ``f`` of
   mappings.py:83-94): every rank sees the full hidden state and its own
   vocabulary shard of the weight; the input gradient is all-reduced;
 * fused, sequence parallel (mappings.py:109-120): every rank holds
-  ``[B, S/2, H]``; the tokens are gathered rank-major, the labels permuted to
+  ``[B, S/tp, H]``; the tokens are gathered rank-major, the labels permuted to
   match, and the input gradient reduce-scattered back to the shards.
 
-Both ranks must return the same loss, equal to the fp64 closed form over the
+Every rank must return the same loss, equal to the fp64 closed form over the
 full vocabulary (oracle ``closed_form`` / ``lmhead_closed_form``) within 1e-5
 relative. The unfused logit gradient of each shard is the matching column
 slice of the full-vocabulary gradient, within one bf16 rounding. The fused
@@ -37,8 +38,7 @@ from oracle import ce_oracle
 
 pytestmark = pytest.mark.gpu
 
-WORLD = 2
-B, S, H, V = 2, 96, 128, 2 * 640
+B, S, H, V = 2, 96, 128, 4 * 320
 
 
 def _free_port() -> int:
@@ -56,18 +56,18 @@ def _inputs():
     return logits, hidden, weight, labels
 
 
-def _worker(rank: int, port: int, out_dir: str) -> None:
+def _worker(rank: int, world: int, port: int, out_dir: str) -> None:
     os.environ["MASTER_ADDR"] = "127.0.0.1"
     os.environ["MASTER_PORT"] = str(port)
-    dist.init_process_group("gloo", rank=rank, world_size=WORLD)
+    dist.init_process_group("gloo", rank=rank, world_size=world)
     try:
         torch.cuda.set_device(0)
         import nmce
         dev = torch.device("cuda:0")
-        ctx = nmce.ParallelContext(rank=rank, world_size=WORLD, tp_size=WORLD, tp_rank=rank,
+        ctx = nmce.ParallelContext(rank=rank, world_size=world, tp_size=world, tp_rank=rank,
                                    pp_size=1, pp_rank=0, dp_size=1, dp_rank=0)
         logits, hidden, weight, labels = _inputs()
-        per = V // WORLD
+        per = V // world
         lo, hi = rank * per, (rank + 1) * per
         t = labels.to(dev)
         res = {}
@@ -86,7 +86,7 @@ def _worker(rank: int, port: int, out_dir: str) -> None:
             head.weight = torch.nn.Parameter(weight[lo:hi].to(dev))
             head.sequence_parallel = sp
             if sp:
-                s2 = S // WORLD
+                s2 = S // world
                 xh = hidden[:, rank * s2:(rank + 1) * s2].contiguous().to(dev)
             else:
                 xh = hidden.to(dev)
@@ -103,26 +103,29 @@ def _worker(rank: int, port: int, out_dir: str) -> None:
         dist.destroy_process_group()
 
 
-@pytest.fixture(scope="module")
-def ranks(tmp_path_factory):
+@pytest.fixture(scope="module", params=[2, 4], ids=["tp2", "tp4"])
+def ranks(request, tmp_path_factory):
     assert torch.cuda.is_available(), "GPU tests need a ROCm device"
-    out = tmp_path_factory.mktemp("tp_gpu")
-    mp.start_processes(_worker, args=(_free_port(), str(out)), nprocs=WORLD, join=True,
+    world = request.param
+    out = tmp_path_factory.mktemp(f"tp_gpu{world}")
+    print(f"[tp_gpu] spawning {world} ranks on cuda:0", flush=True)
+    mp.start_processes(_worker, args=(world, _free_port(), str(out)), nprocs=world, join=True,
                        start_method="spawn")
-    return [dict(np.load(out / f"rank{r}.npz")) for r in range(WORLD)]
+    return [dict(np.load(out / f"rank{r}.npz")) for r in range(world)]
 
 
 def _nrel(got, want):
     return np.linalg.norm(got - want) / np.linalg.norm(want)
 
 
-def test_unfused_two_ranks(ranks):
+def test_unfused_tp_ranks(ranks):
     logits, _, _, labels = _inputs()
     n = B * S
     x = logits.reshape(n, V).double().numpy()
     loss, grad = ce_oracle.closed_form(x, labels.reshape(-1).numpy(), 1.0 / n)
-    per = V // WORLD
-    for r in range(WORLD):
+    world = len(ranks)
+    per = V // world
+    for r in range(world):
         assert abs(ranks[r]["u_loss"] - loss.mean()) <= 1e-5 * loss.mean()
         got = ranks[r]["u_grad"].reshape(n, per).astype(np.float64)
         want = grad[:, r * per:(r + 1) * per]
@@ -131,7 +134,7 @@ def test_unfused_two_ranks(ranks):
 
 
 @pytest.mark.parametrize("tag", ["tp", "sp"])
-def test_fused_two_ranks(ranks, tag):
+def test_fused_tp_ranks(ranks, tag):
     _, hidden, weight, labels = _inputs()
     n = B * S
     X = hidden.reshape(n, H).double().numpy()
@@ -139,9 +142,10 @@ def test_fused_two_ranks(ranks, tag):
     loss, _, dx, dw = ce_oracle.lmhead_closed_form(X, W, labels.reshape(-1).numpy(),
                                                    np.full(n, 1.0 / n))
     dx = dx.reshape(B, S, H)
-    per = V // WORLD
-    s2 = S // WORLD
-    for r in range(WORLD):
+    world = len(ranks)
+    per = V // world
+    s2 = S // world
+    for r in range(world):
         assert abs(ranks[r][f"{tag}_loss"] - loss.mean()) <= 1e-5 * loss.mean()
         want_dx = dx if tag == "tp" else dx[:, r * s2:(r + 1) * s2]
         assert _nrel(ranks[r][f"{tag}_dx"], want_dx) <= 6e-3
