@@ -284,12 +284,17 @@ def test_bwd_dz_buffers():
         assert not rawt[:, n:ldt].any(), f"chunk {c}: token padding of dZ^T"
 
 
-def test_fused_two_shards_combined():
+@pytest.mark.parametrize("v,chunk", [(1024, 0), (1000, 192)])
+def test_fused_two_shards_combined(v, chunk):
     """TP=2 split of the vocabulary, shards combined locally: same loss and the
-    same gradients (dW rows per shard, dH summed) as the full vocabulary."""
+    same gradients (dW rows per shard, dH summed) as the full vocabulary. The
+    second case has ragged 500-row shards recomputed in chunks (the 192 rows
+    asked for round up to one 256-row tile), so each shard's second chunk is
+    ragged and shard 1's chunks start at global ids that are not multiples of
+    128."""
     from nmce import _lib as L
     lib = L.load()
-    n, h, v = 300, 128, 1024
+    n, h = 300, 128
     x, w, t = make_inputs(n, h, v, seed=5, w_std=0.5)
     half = v // 2
     stats = [run_fused(x, w[r * half:(r + 1) * half], t, vstart=r * half, tp_stats=True)
@@ -312,12 +317,12 @@ def test_fused_two_shards_combined():
         dw = torch.empty((half, h), dtype=torch.bfloat16, device=DEV)
         go = torch.full((1,), 1.0 / n, dtype=torch.float32, device=DEV)
         td = t.to(DEV)
-        ws = torch.empty(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, h, half, 0), dtype=torch.uint8,
-                         device=DEV)
+        ws = torch.empty(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, h, half, chunk),
+                         dtype=torch.uint8, device=DEV)
         L.check(lib.nmce_lmhead_ce_bwd(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, half,
                                        td.data_ptr(), r * half, out[1].data_ptr(),
                                        out[2].data_ptr(), go.data_ptr(), 0, dx.data_ptr(),
-                                       dw.data_ptr(), 0, ws.data_ptr(), ws.numel(),
+                                       dw.data_ptr(), chunk, ws.data_ptr(), ws.numel(),
                                        L.stream_handle(torch.device(DEV))), "bwd")
         dxs.append(dx.float().cpu().numpy())
         dws.append(dw.float().cpu().numpy())
