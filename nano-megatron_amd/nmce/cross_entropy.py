@@ -24,6 +24,10 @@ Differences from the reference, all deliberate:
 * With ``tp_size > 1`` the three dependent all-reduces (:23, :38, :43) become
   one all-gather of packed ``[3, tokens]`` statistics followed by a local
   combine.
+* The wrapper's ``loss.mean()`` (:85) is taken inside its own Function, whose
+  backward hands the loss kernel the mean's scalar gradient and the token
+  count: the kernel divides in fp32 exactly as ``MeanBackward`` would, so the
+  gradient is bit-identical and the expand/divide pass is gone.
 
 There is no CPU path: the tensors must be on a ROCm device and ``libnmce.so``
 must be built; anything else raises.
