@@ -443,15 +443,25 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
     const int tloc = wn * kWaveN + 32 * fn + (lane & 31);
     const int64_t tok = n0 + tloc;
     const bool tok_ok = tok < N;
-    float mc = 0.0f, scale = 0.0f, g = 0.0f;
+    float mc = 0.0f, scale = 0.0f, g = 0.0f, S = 1.0f;
     int tl = -1;  // target row within this wave's rows, or -1
     if (tok_ok) {
       g = gout[tok * gout_stride];
+      S = gsum[tok];
       mc = gmax[tok] * kLog2e;
-      scale = g / gsum[tok];
+      scale = g / S;
       const int64_t t = target[tok] - vfirst - vrow0;
       tl = (t >= 0 && t < valid_rows) ? static_cast<int>(t) : -1;
     }
+    // The target row follows the reference's order, (softmax - 1) * g
+    // (cross_entropy.py:58-64): when its softmax is close to 1 the difference
+    // keeps its relative accuracy, and it is exactly 0 when the softmax is 1.
+    float zt = 0.0f;
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) zt = (acc_row(fm, e, fhalf) == tl) ? acc.c[fm][fn][e] : zt;
+    const float dt = (exp2_hw(fmaf(zt, kLog2e, -mc)) / S - 1.0f) * g;
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm) {
       float d[16];
@@ -459,7 +469,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
       for (int e = 0; e < 16; ++e) {
         const int r = acc_row(fm, e, fhalf);
         float p = exp2_hw(fmaf(acc.c[fm][fn][e], kLog2e, -mc)) * scale;
-        p -= (r == tl) ? g : 0.0f;
+        p = (r == tl) ? dt : p;
         d[e] = (tok_ok && r < valid_rows) ? p : 0.0f;
       }
       // Into the LDS tile as (even, odd) vocabulary-row pairs of one token:

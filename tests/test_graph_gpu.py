@@ -48,7 +48,7 @@ def test_unfused_step_replays_exactly():
         logits.grad = None
         loss = nmce.vocab_parallel_cross_entropy(logits, target, 0, v, ctx, validate=False)
         loss.backward()
-        return loss
+        return loss.detach()  # keep no autograd graph alive between steps
 
     graph, static_loss = _capture(step)
     g = torch.Generator().manual_seed(3)
@@ -99,7 +99,7 @@ def test_fused_step_replays_exactly():
         loss = nmce.lmhead_vocab_parallel_cross_entropy(hidden, weight, target, 0, v, ctx,
                                                         vocab_chunk=2048, validate=False)
         loss.backward()
-        return loss
+        return loss.detach()
 
     graph, static_loss = _capture(step)
     g = torch.Generator().manual_seed(4)

@@ -1,0 +1,109 @@
+"""Seeded sweep of the fused LM head + loss over shapes, shard splits and
+backward chunks, through the C ABI.
+
+Each case draws tokens n, hidden size h (a multiple of 64, the C ABI's
+granularity), a shard width and a TP degree (the vocabulary is tp shards of
+that width, combined locally as the TP exchange would), a backward chunk and
+either the mean's scalar gradient or a per-token one with mixed signs. The
+combined loss must equal the fp64 closed form over the full vocabulary within
+1e-5 relative; dW (the shards' rows stacked) and dH (the shards' partial sums
+added) are checked as in test_lmhead_gpu.py: norm-relative 4e-3 against the
+exact fp64 product, element-wise within one bf16 rounding plus a one-ulp dZ
+flip per term of the product taken with dZ rounded to bf16.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ce_oracle
+from test_lmhead_gpu import DEV, GradRef, check_grad
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(count=24, seed=2024):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        tp = int(rng.choice([1, 1, 2, 3]))
+        per = int(rng.choice([1, 7, 100, 128, 255, 256, 300, 777, 1024, 1500]))
+        n = int(rng.choice([1, 3, 63, 64, 65, 200, 256, 300, 511]))
+        h = int(rng.choice([64, 128, 192, 320]))
+        chunk = int(rng.choice([0, 256, 512]))
+        per_token = bool(rng.integers(0, 2))
+        out.append((i, n, h, per, tp, chunk, per_token))
+    return out
+
+
+def _run_shards(x, w, t, tp, chunk, go):
+    """Forward stats per shard, local combine, backward per shard."""
+    from nmce import _lib as L
+    lib = L.load()
+    n, h = x.shape
+    v = w.shape[0]
+    per = v // tp
+    stream = L.stream_handle(torch.device(DEV))
+    xd, td = x.to(DEV), t.to(DEV)
+    stats = torch.empty((tp, 3, n), dtype=torch.float32, device=DEV)
+    for r in range(tp):
+        wd = w[r * per:(r + 1) * per].contiguous().to(DEV)
+        ws = torch.empty(max(lib.nmce_lmhead_ce_fwd_workspace_bytes(n, h, per), 16),
+                         dtype=torch.uint8, device=DEV)
+        L.check(lib.nmce_lmhead_ce_fwd_stats(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h,
+                                             per, td.data_ptr(), r * per,
+                                             stats[r, 0].data_ptr(), stats[r, 1].data_ptr(),
+                                             stats[r, 2].data_ptr(), ws.data_ptr(), ws.numel(),
+                                             stream), "fwd_stats")
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    b = stats.data_ptr()
+    L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, tp, 3 * n, n, out[0].data_ptr(),
+                                out[1].data_ptr(), out[2].data_ptr(), stream), "combine")
+    if go is None:
+        god, gs = torch.full((1,), 1.0 / n, dtype=torch.float32, device=DEV), 0
+    else:
+        god, gs = torch.as_tensor(go, dtype=torch.float32).to(DEV), 1
+    dxs, dws = [], []
+    for r in range(tp):
+        wd = w[r * per:(r + 1) * per].contiguous().to(DEV)
+        dx = torch.empty((n, h), dtype=torch.bfloat16, device=DEV)
+        dw = torch.empty((per, h), dtype=torch.bfloat16, device=DEV)
+        ws = torch.empty(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, h, per, chunk),
+                         dtype=torch.uint8, device=DEV)
+        L.check(lib.nmce_lmhead_ce_bwd(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, per,
+                                       td.data_ptr(), r * per, out[1].data_ptr(),
+                                       out[2].data_ptr(), god.data_ptr(), gs, dx.data_ptr(),
+                                       dw.data_ptr(), chunk, ws.data_ptr(), ws.numel(), stream),
+                "bwd")
+        dxs.append(dx.double().cpu().numpy())
+        dws.append(dw.double().cpu().numpy())
+    torch.cuda.synchronize()
+    return out[0].cpu().numpy(), sum(dxs), np.concatenate(dws)
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: f"case{c[0]}")
+def test_fused_sweep(case):
+    i, n, h, per, tp, chunk, per_token = case
+    v = per * tp
+    print(f"[sweep] case {i}: n={n} h={h} shard={per} tp={tp} chunk={chunk} "
+          f"per_token={per_token}", flush=True)
+    g = torch.Generator().manual_seed(1000 + i)
+    x = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    w = (torch.randn(v, h, generator=g) * 0.4).to(torch.bfloat16)
+    # targets over the whole vocabulary, plus every shard's edges when they fit
+    t = torch.randint(0, v, (n,), generator=g)
+    edges = [e for r in range(tp) for e in (r * per, r * per + per - 1)]
+    for k, e in enumerate(edges[:n]):
+        t[k] = e
+    go = None
+    if per_token:
+        go = (torch.rand(n, generator=g) * 2.0 - 0.5).numpy()
+    loss, dx, dw = _run_shards(x, w, t, tp, chunk, go)
+    X, W = x.double().numpy(), w.double().numpy()
+    gv = np.full(n, 1.0 / n) if go is None else go.astype(np.float64)
+    rl, dz, _, _ = ce_oracle.lmhead_closed_form(X, W, t.numpy(), gv)
+    np.testing.assert_allclose(loss, rl, rtol=1e-5, atol=1e-6)
+    check_grad(dx, GradRef(dz, W), f"case {i} dH")
+    check_grad(dw, GradRef(dz.T.copy(), X), f"case {i} dW")
