@@ -1,5 +1,6 @@
-"""Seeded sweep of the fused LM head + loss over shapes, shard splits and
-backward chunks, through the C ABI.
+"""Seeded sweeps of both loss paths through the C ABI.
+
+Fused LM head + loss, over shapes, shard splits and backward chunks:
 
 Each case draws tokens n, hidden size h (a multiple of 64, the C ABI's
 granularity), a shard width and a TP degree (the vocabulary is tp shards of
@@ -10,6 +11,9 @@ combined loss must equal the fp64 closed form over the full vocabulary within
 added) are checked as in test_lmhead_gpu.py: norm-relative 4e-3 against the
 exact fp64 product, element-wise within one bf16 rounding plus a one-ulp dZ
 flip per term of the product taken with dZ rounded to bf16.
+
+Unfused loss, over dtypes, ragged shard widths, padded and misaligned row
+strides, TP splits and gradient forms (tolerances in its docstring).
 """
 
 from __future__ import annotations
@@ -107,3 +111,82 @@ def test_fused_sweep(case):
     np.testing.assert_allclose(loss, rl, rtol=1e-5, atol=1e-6)
     check_grad(dx, GradRef(dz, W), f"case {i} dH")
     check_grad(dw, GradRef(dz.T.copy(), X), f"case {i} dW")
+
+
+def _unfused_cases(count=24, seed=77):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+        n = int(rng.choice([1, 2, 17, 64, 100, 1000]))
+        per = int(rng.choice([1, 2, 7, 8, 9, 15, 16, 17, 100, 1023, 1024, 1025, 4097]))
+        tp = int(rng.choice([1, 2, 3]))
+        pad = int(rng.choice([0, 1, 8, 13]))
+        offset = int(rng.choice([0, 1, 3]))
+        per_token = bool(rng.integers(0, 2))
+        out.append((i, dtype, n, per, tp, pad, offset, per_token))
+    return out
+
+
+@pytest.mark.parametrize("case", _unfused_cases(), ids=lambda c: f"case{c[0]}")
+def test_unfused_sweep(case):
+    """The unfused kernels through the C ABI on shards that are column slices of
+    one padded, possibly misaligned slab: row stride V_full + pad, the slab
+    starting ``offset`` elements into its allocation (so rows may sit off the
+    16-byte grid and take the element-wise paths), tp shards combined locally,
+    the mean's scalar gradient or a per-token one. Loss within 1e-5 relative of
+    the oracle's sharded fp64 form; fp32 gradients within 1e-5 relative, bf16
+    gradients within one bf16 ulp."""
+    from _util import assert_bf16_close, assert_close_rel
+    from nmce import _lib as L
+    i, dtype, n, per, tp, pad, offset, per_token = case
+    print(f"[sweep] unfused case {i}: {dtype} n={n} shard={per} tp={tp} pad={pad} "
+          f"offset={offset} per_token={per_token}", flush=True)
+    lib = L.load()
+    v = per * tp
+    ld = v + pad
+    g = torch.Generator().manual_seed(5000 + i)
+    x = (torch.randn(n, v, generator=g) * 2.0).to(dtype)
+    t = torch.randint(0, v, (n,), generator=g)
+    edges = [e for r in range(tp) for e in (r * per, r * per + per - 1)]
+    for k, e in enumerate(edges[:n]):
+        t[k] = e
+    go = (torch.rand(n, generator=g) * 2.0 - 0.5) if per_token else None
+    store = torch.zeros(offset + n * ld, dtype=dtype, device=DEV)
+    slab = store[offset:].view(n, ld)
+    slab[:, :v] = x.to(DEV)
+    td = t.to(DEV)
+    stream = L.stream_handle(torch.device(DEV))
+    code = L.dtype_code(dtype)
+    stats = torch.empty((tp, 3, n), dtype=torch.float32, device=DEV)
+    for r in range(tp):
+        sh = slab[:, r * per:(r + 1) * per]
+        L.check(lib.nmce_ce_fwd_stats(sh.data_ptr(), code, n, per, ld, td.data_ptr(), r * per,
+                                      stats[r, 0].data_ptr(), stats[r, 1].data_ptr(),
+                                      stats[r, 2].data_ptr(), stream), "stats")
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    b = stats.data_ptr()
+    L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, tp, 3 * n, n, out[0].data_ptr(),
+                                out[1].data_ptr(), out[2].data_ptr(), stream), "combine")
+    if go is None:
+        god, gs = torch.full((1,), 1.0 / n, dtype=torch.float32, device=DEV), 0
+    else:
+        god, gs = go.to(DEV), 1
+    grads = []
+    for r in range(tp):
+        sh = slab[:, r * per:(r + 1) * per]
+        gr = torch.empty((n, per), dtype=dtype, device=DEV)
+        L.check(lib.nmce_ce_bwd(sh.data_ptr(), gr.data_ptr(), code, n, per, ld, per,
+                                td.data_ptr(), r * per, out[1].data_ptr(), out[2].data_ptr(),
+                                god.data_ptr(), gs, stream), "bwd")
+        grads.append(gr)
+    torch.cuda.synchronize()
+    gov = np.full(n, 1.0 / n) if go is None else go.double().numpy()
+    ol, og, _, _ = ce_oracle.sharded(x.double().numpy(), t.numpy(), tp, gov)
+    assert_close_rel(out[0].cpu().numpy(), ol, 1e-5, 1e-6, what=f"case {i} loss")
+    for r in range(tp):
+        got = grads[r].double().cpu().numpy()
+        if dtype == torch.float32:
+            assert_close_rel(got, og[r], 1e-5, 1e-12, what=f"case {i} grad shard {r}")
+        else:
+            assert_bf16_close(got, og[r], what=f"case {i} bf16 grad shard {r}", atol=1e-30)
