@@ -528,6 +528,12 @@ def test_fused_head_module_fp32_tied_weight_under_autocast():
     assert nrel <= 8e-3, f"tied fp32 weight gradient norm-relative error {nrel:.3e}"
     with pytest.raises(TypeError, match="bf16"):
         head(x.detach(), t.to(DEV))
+    # sequence parallelism at TP = 1: the rank-major token order is the natural
+    # one, so the loss is the same
+    head.sequence_parallel = True
+    with torch.autocast("cuda", dtype=torch.bfloat16):
+        loss_sp = head(x.detach(), t.to(DEV))
+    assert loss_sp.item() == loss.item()
 
 
 def test_fused_empty_batch():
