@@ -5,13 +5,15 @@
 //                     target logit (cross_entropy.py:21, :28-36, :40-41)
 //   ce_combine_kernel cross-shard merge and per-token loss, done locally
 //                     (the all-reduces at :22-23, :37-38, :42-43 and :45)
-//   ce_bwd_kernel     one read + one write pass: softmax - onehot, scaled by
-//                     grad_output, written in the logits dtype, optionally in
-//                     place (:53-65 plus the cast back of :83)
+//   ce_bwd_flat_kernel / ce_bwd_kernel
+//                     one read + one write pass: softmax - onehot, scaled by
+//                     grad_output (optionally divided by the token count, for
+//                     the wrapper's mean), written in the logits dtype,
+//                     optionally in place (:53-65 plus the cast back of :83)
 //
 // Forward layout: one 1024-lane workgroup per row (token). A row of 50304
 // bf16 is 98 KiB; the workgroup streams it with 16-byte non-temporal loads,
-// four in flight per lane, folding them into per-lane (max, sumexp) pairs that
+// two in flight per lane, folding them into per-lane (max, sumexp) pairs that
 // are merged with DPP inside each wave and through LDS across the 16 waves.
 // Big workgroups keep fewer rows open at once (512 on 256 CUs), which keeps
 // the HBM access stream close to sequential.
