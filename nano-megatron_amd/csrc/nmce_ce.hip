@@ -49,10 +49,9 @@ __device__ __forceinline__ void online_fold(float& m, float& s, const float* f) 
 #pragma unroll
   for (int k = 1; k < K; ++k) cm = fmaxf(cm, f[k]);
   const float nm = fmaxf(m, cm);
-  const float nmc = nm * kLog2e;
   float e[K];
 #pragma unroll
-  for (int k = 0; k < K; ++k) e[k] = exp2_hw(fmaf(f[k], kLog2e, -nmc));
+  for (int k = 0; k < K; ++k) e[k] = exp_shift(f[k], nm);
 #pragma unroll
   for (int w = 1; w < K; w *= 2) {
 #pragma unroll
@@ -199,8 +198,8 @@ __global__ __launch_bounds__(kValidateThreads) void validate_targets_kernel(
 
 // grad = (exp(x - M) / S - onehot) * g for one element; the onehot column
 // follows the reference's order: softmax first, minus one, then times g.
-__device__ __forceinline__ float target_grad(float x, float mc, float S, float g) {
-  return (exp2_hw(fmaf(x, kLog2e, -mc)) / S - 1.0f) * g;
+__device__ __forceinline__ float target_grad(float x, float M, float S, float g) {
+  return (exp_shift(x, M) / S - 1.0f) * g;
 }
 
 template <typename T, bool kVec, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
@@ -218,7 +217,6 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const float M = g_max[row];
     const float S = g_sum[row];
     const float go = gout[row * gstride] / gdiv;
-    const float mc = M * kLog2e;
     const float scale = go / S;
     const int64_t lt = target[row] - vstart;  // owned iff 0 <= lt < V
 
@@ -239,12 +237,12 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
           float f[EPV], y[EPV];
           E::unpack(v[u], f);
 #pragma unroll
-          for (int k = 0; k < EPV; ++k) y[k] = exp2_hw(fmaf(f[k], kLog2e, -mc)) * scale;
+          for (int k = 0; k < EPV; ++k) y[k] = exp_shift(f[k], M) * scale;
           const int64_t d = lt_body - (i + u * kBlock) * EPV;
           if (static_cast<uint64_t>(d) < static_cast<uint64_t>(EPV)) {
 #pragma unroll
             for (int k = 0; k < EPV; ++k)
-              if (k == d) y[k] = target_grad(f[k], mc, S, go);
+              if (k == d) y[k] = target_grad(f[k], M, S, go);
           }
           store_stream(gp + i + u * kBlock, E::pack(y));
         }
@@ -253,12 +251,12 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
         float f[EPV], y[EPV];
         E::unpack(load_stream(vp + i), f);
 #pragma unroll
-        for (int k = 0; k < EPV; ++k) y[k] = exp2_hw(fmaf(f[k], kLog2e, -mc)) * scale;
+        for (int k = 0; k < EPV; ++k) y[k] = exp_shift(f[k], M) * scale;
         const int64_t d = lt_body - i * EPV;
         if (static_cast<uint64_t>(d) < static_cast<uint64_t>(EPV)) {
 #pragma unroll
           for (int k = 0; k < EPV; ++k)
-            if (k == d) y[k] = target_grad(f[k], mc, S, go);
+            if (k == d) y[k] = target_grad(f[k], M, S, go);
         }
         store_stream(gp + i, E::pack(y));
       }
@@ -267,14 +265,14 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
       else if (tid >= EPV && tid - EPV < V - body_end) j = body_end + (tid - EPV);
       if (j >= 0) {
         const float f = E::load1(xr + j);
-        E::store1(gr + j, j == lt ? target_grad(f, mc, S, go)
-                                  : exp2_hw(fmaf(f, kLog2e, -mc)) * scale);
+        E::store1(gr + j, j == lt ? target_grad(f, M, S, go)
+                                  : exp_shift(f, M) * scale);
       }
     } else {
       for (int64_t j = tid; j < V; j += kBlock) {
         const float f = E::load1(xr + j);
-        E::store1(gr + j, j == lt ? target_grad(f, mc, S, go)
-                                  : exp2_hw(fmaf(f, kLog2e, -mc)) * scale);
+        E::store1(gr + j, j == lt ? target_grad(f, M, S, go)
+                                  : exp_shift(f, M) * scale);
       }
     }
   }
@@ -314,17 +312,16 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     const float M = g_max[row];
     const float S = g_sum[row];
     const float go = gstride == 0 ? g0 : gout[row * gstride] / gdiv;
-    const float mc = M * kLog2e;
     const float scale = go / S;
     const int64_t d = target[row] - vstart - cols[u];
     float f32[EPV], y[EPV];
     E::unpack(v[u], f32);
 #pragma unroll
-    for (int k = 0; k < EPV; ++k) y[k] = exp2_hw(fmaf(f32[k], kLog2e, -mc)) * scale;
+    for (int k = 0; k < EPV; ++k) y[k] = exp_shift(f32[k], M) * scale;
     if (static_cast<uint64_t>(d) < static_cast<uint64_t>(EPV)) {
 #pragma unroll
       for (int k = 0; k < EPV; ++k)
-        if (k == d) y[k] = target_grad(f32[k], mc, S, go);
+        if (k == d) y[k] = target_grad(f32[k], M, S, go);
     }
     store_stream(reinterpret_cast<u32x4*>(g + row * ldg + cols[u]), E::pack(y));
   }

@@ -23,6 +23,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // v_exp_f32: 2^x, about 1 ulp; 2^-inf = 0.
 __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// exp(x - m) as 2^((x - m) log2 e). The difference is taken first, as the
+// reference's exp(x - max) does: x = m gives exactly 1, and the argument's
+// rounding error is relative to x - m rather than to x. (Folding the shift
+// into one fma, 2^(x log2 e - m log2 e), leaves up to half an ulp of
+// x log2 e in the argument: about 1e-6 relative on the dominant term of a row
+// whose logits are near 30, and so about 1e-6 absolute on a confident
+// token's loss.)
+__device__ __forceinline__ float exp_shift(float x, float m) { return exp2_hw((x - m) * kLog2e); }
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {

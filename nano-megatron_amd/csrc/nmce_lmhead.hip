@@ -334,14 +334,13 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
         pick = (r == tl) ? z : pick;
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mc = mx * kLog2e;
     float s = 0.0f;
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = acc_row(fm, e, fhalf);
-        const float p = exp2_hw(fmaf(acc.c[fm][fn][e], kLog2e, -mc));
+        const float p = exp_shift(acc.c[fm][fn][e], mx);
         s += (r < valid_rows) ? p : 0.0f;
       }
     s += __shfl_xor(s, 32);
@@ -443,12 +442,12 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
     const int tloc = wn * kWaveN + 32 * fn + (lane & 31);
     const int64_t tok = n0 + tloc;
     const bool tok_ok = tok < N;
-    float mc = 0.0f, scale = 0.0f, g = 0.0f, S = 1.0f;
+    float M = 0.0f, scale = 0.0f, g = 0.0f, S = 1.0f;
     int tl = -1;  // target row within this wave's rows, or -1
     if (tok_ok) {
       g = gout[tok * gout_stride];
       S = gsum[tok];
-      mc = gmax[tok] * kLog2e;
+      M = gmax[tok];
       scale = g / S;
       const int64_t t = target[tok] - vfirst - vrow0;
       tl = (t >= 0 && t < valid_rows) ? static_cast<int>(t) : -1;
@@ -461,14 +460,14 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
     for (int fm = 0; fm < kFM; ++fm)
 #pragma unroll
       for (int e = 0; e < 16; ++e) zt = (acc_row(fm, e, fhalf) == tl) ? acc.c[fm][fn][e] : zt;
-    const float dt = (exp2_hw(fmaf(zt, kLog2e, -mc)) / S - 1.0f) * g;
+    const float dt = (exp_shift(zt, M) / S - 1.0f) * g;
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm) {
       float d[16];
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = acc_row(fm, e, fhalf);
-        float p = exp2_hw(fmaf(acc.c[fm][fn][e], kLog2e, -mc)) * scale;
+        float p = exp_shift(acc.c[fm][fn][e], M) * scale;
         p = (r == tl) ? dt : p;
         d[e] = (tok_ok && r < valid_rows) ? p : 0.0f;
       }
