@@ -56,15 +56,24 @@ int nmce_version(void);
  * Replaces cross_entropy.py:21 (row max), :28-36 (masked target pick) and
  * :40-41 (exp-sum) for one vocabulary shard.
  *
- *   row_max[r]    = max_j x[r, j]                         (fp32)
- *   row_sumexp[r] = sum_j exp(x[r, j] - row_max[r])        (fp32)
- *   target_logit[r] = x[r, target[r]-vocab_start] if the target is in this
- *                     shard, else 0.0  (raw logit, not shifted)
+ *   row_max[r]       = max_j x[r, j]                            (fp32)
+ *   row_sumexp_m1[r] = sum_j exp(x[r, j] - row_max[r]) - 1      (fp32)
+ *   target_logit[r]  = x[r, target[r]-vocab_start] if the target is in this
+ *                      shard, else 0.0  (raw logit, not shifted)
+ * The exp-sum is carried minus the maximum's own term (exactly 1), so that
+ * for a confident token, whose other terms are all small, it keeps its
+ * relative precision; the loss and the target column's gradient are formed
+ * from it with log1p and expm1. For fp32 logits the sum is accumulated with
+ * the terms equal to 1 kept apart (relative error a few 2^-24); bf16 rows
+ * accumulate the plain sum and subtract 1 per lane (absolute error a few
+ * 2^-24), which keeps the bf16 pass within its memory-bound time.
+ * A row whose shard holds only -inf gives row_max = -1e38 and
+ * row_sumexp_m1 = -1 (an empty sum), which the combine gives no weight.
  * dtype: NMCE_F32 or NMCE_BF16 (math is fp32 either way).
  */
 int nmce_ce_fwd_stats(const void* logits, int dtype, int64_t n_rows,
                       int64_t vocab_local, int64_t ld, const int64_t* target,
-                      int64_t vocab_start, float* row_max, float* row_sumexp,
+                      int64_t vocab_start, float* row_max, float* row_sumexp_m1,
                       float* target_logit, void* stream);
 
 /*
@@ -72,11 +81,11 @@ int nmce_ce_fwd_stats(const void* logits, int dtype, int64_t n_rows,
  * in. Same results as nmce_ce_fwd_stats(vocab_start = 0) followed by
  * nmce_ce_combine(tp = 1), bit for bit, in one read pass and one launch.
  * Replaces cross_entropy.py:17-50 at world_size == 1.
- *   g_max[r], g_sumexp[r], loss[r] as defined for nmce_ce_combine.
+ *   g_max[r], g_sumexp_m1[r], loss[r] as defined for nmce_ce_combine.
  */
 int nmce_ce_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
                 int64_t ld, const int64_t* target, float* loss, float* g_max,
-                float* g_sumexp, void* stream);
+                float* g_sumexp_m1, void* stream);
 
 /*
  * Cross-shard combine of per-shard statistics, done locally.
@@ -85,17 +94,19 @@ int nmce_ce_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab,
  *
  * Shard k's statistic for row r sits at [k*shard_stride + r] of each input
  * (a [tp, ...] stack, e.g. the all-gathered [tp, 3, n_rows] buffer of a real
- * TP group with row_max = base, row_sumexp = base + n_rows, target_logit =
+ * TP group with row_max = base, row_sumexp_m1 = base + n_rows, target_logit =
  * base + 2*n_rows and shard_stride = 3*n_rows).
  *
- *   g_max[r]    = max_k row_max[k, r]
- *   g_sumexp[r] = sum_k row_sumexp[k, r] * exp(row_max[k, r] - g_max[r])
- *   loss[r]     = log(g_sumexp[r]) - (sum_k target_logit[k, r] - g_max[r])
- * Any of loss / g_max / g_sumexp may be NULL if not wanted.
+ *   g_max[r]       = max_k row_max[k, r]
+ *   g_sumexp_m1[r] = sum_k (1 + row_sumexp_m1[k, r]) * exp(row_max[k, r] - g_max[r]) - 1
+ *                    (formed without the cancellation: a shard at the maximum
+ *                    adds its row_sumexp_m1, each further one its full sum)
+ *   loss[r]        = log1p(g_sumexp_m1[r]) - (sum_k target_logit[k, r] - g_max[r])
+ * Any of loss / g_max / g_sumexp_m1 may be NULL if not wanted.
  */
-int nmce_ce_combine(const float* row_max, const float* row_sumexp,
+int nmce_ce_combine(const float* row_max, const float* row_sumexp_m1,
                     const float* target_logit, int tp, int64_t shard_stride,
-                    int64_t n_rows, float* loss, float* g_max, float* g_sumexp,
+                    int64_t n_rows, float* loss, float* g_max, float* g_sumexp_m1,
                     void* stream);
 
 /*
@@ -114,8 +125,12 @@ int nmce_validate_targets(const int64_t* target, int64_t n_rows,
  * Replaces cross_entropy.py:53-65 plus the autograd cast back to the logits
  * dtype (the .float() at :83).
  *
- *   grad[r, j] = (exp(x[r, j] - g_max[r]) / g_sumexp[r]
+ *   grad[r, j] = (exp(x[r, j] - g_max[r]) / (1 + g_sumexp_m1[r])
  *                 - [j == target[r] - vocab_start]) * grad_output[r*gout_stride]
+ * with the target column, when it holds the row maximum, formed as
+ *   -g_sumexp_m1[r] / (1 + g_sumexp_m1[r]) * g,
+ * the same value without the cancellation of softmax - 1 near 1 (a target
+ * below the maximum has softmax <= 1/2, where the plain form is exact enough).
  * gout_stride = 0 broadcasts grad_output[0] to every row (the loss.mean()
  * case). grad may equal logits (in place, ld_grad == ld); otherwise the two
  * must not overlap. grad has the same dtype as logits.
@@ -123,7 +138,7 @@ int nmce_validate_targets(const int64_t* target, int64_t n_rows,
 int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows,
                 int64_t vocab_local, int64_t ld, int64_t ld_grad,
                 const int64_t* target, int64_t vocab_start, const float* g_max,
-                const float* g_sumexp, const float* grad_output,
+                const float* g_sumexp_m1, const float* grad_output,
                 int64_t gout_stride, void* stream);
 
 /*
@@ -138,7 +153,7 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows,
 int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows,
                        int64_t vocab_local, int64_t ld, int64_t ld_grad,
                        const int64_t* target, int64_t vocab_start, const float* g_max,
-                       const float* g_sumexp, const float* grad_output,
+                       const float* g_sumexp_m1, const float* grad_output,
                        int64_t gout_stride, float gout_div, void* stream);
 
 /*
@@ -170,12 +185,13 @@ int64_t nmce_lmhead_ce_fwd_workspace_bytes(int64_t n_rows, int64_t hidden_size,
 /*
  * Per-shard statistics of the logits hidden @ weight^T, as nmce_ce_fwd_stats
  * computes them for a stored logit slab (cross_entropy.py:21, :28-36,
- * :40-41 on the shard [vocab_start, vocab_start + vocab_local)). Combine the
+ * :40-41 on the shard [vocab_start, vocab_start + vocab_local)), the exp-sum
+ * minus one accumulated with the terms equal to 1 kept apart. Combine the
  * shards with nmce_ce_combine (tp = 1 for a single shard).
  */
 int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, int64_t n_rows,
                              int64_t hidden_size, int64_t vocab_local, const int64_t* target,
-                             int64_t vocab_start, float* row_max, float* row_sumexp,
+                             int64_t vocab_start, float* row_max, float* row_sumexp_m1,
                              float* target_logit, void* workspace, int64_t workspace_bytes,
                              void* stream);
 
@@ -211,8 +227,9 @@ int nmce_lmhead_ce_bwd_prepare(const void* hidden, const void* weight, int dtype
 /*
  * Step 2, once per chunk c (rows [c*chunk, c*chunk + chunk) of the shard):
  * recompute that slice of the logits and write the logit gradient
- *   dZ[r, j] = (exp(z[r, j] - g_max[r]) / g_sumexp[r]
+ *   dZ[r, j] = (exp(z[r, j] - g_max[r]) / (1 + g_sumexp_m1[r])
  *               - [j == target[r] - vocab_start]) * grad_output[r*gout_stride]
+ * (target column without cancellation, as in nmce_ce_bwd)
  * as bf16 into the workspace's dZ^T and dZ (zeros in their padding). The
  * caller then forms grad_weight rows = dZ^T_c X and grad_hidden += dZ_c W_c
  * (e.g. with a library GEMM on X^T and W^T) before the next chunk overwrites
@@ -221,7 +238,7 @@ int nmce_lmhead_ce_bwd_prepare(const void* hidden, const void* weight, int dtype
  */
 int nmce_lmhead_ce_bwd_dz(const void* hidden, const void* weight, int dtype, int64_t n_rows,
                           int64_t hidden_size, int64_t vocab_local, const int64_t* target,
-                          int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                          int64_t vocab_start, const float* g_max, const float* g_sumexp_m1,
                           const float* grad_output, int64_t gout_stride, int64_t vocab_chunk,
                           int64_t chunk_index, void* workspace, int64_t workspace_bytes,
                           void* stream);
@@ -229,20 +246,20 @@ int nmce_lmhead_ce_bwd_dz(const void* hidden, const void* weight, int dtype, int
 /*
  * Backward of the fused LM head + loss (cross_entropy.py:53-65 followed by
  * the matmul backward of model.py:192):
- *   dZ[r, j]        = (exp(z[r, j] - g_max[r]) / g_sumexp[r]
+ *   dZ[r, j]        = (exp(z[r, j] - g_max[r]) / (1 + g_sumexp_m1[r])
  *                      - [j == target[r] - vocab_start]) * grad_output[r*gout_stride]
  *   grad_hidden     = dZ @ weight          [n_rows, hidden_size] bf16
  *   grad_weight     = dZ^T @ hidden        [vocab_local, hidden_size] bf16
  * with z = hidden @ weight^T recomputed chunk by chunk (vocab_chunk rows of
  * the shard at a time) and dZ rounded to bf16 before the two products, as the
  * reference's autocast matmul backward consumes a bf16 gradient. g_max and
- * g_sumexp are the combined statistics of the forward (nmce_ce_combine).
+ * g_sumexp_m1 are the combined statistics of the forward (nmce_ce_combine).
  * grad_hidden is this shard's contribution only (the TP all-reduce of the
  * input gradient, mappings.py:83-94, belongs to the caller).
  */
 int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_t n_rows,
                        int64_t hidden_size, int64_t vocab_local, const int64_t* target,
-                       int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                       int64_t vocab_start, const float* g_max, const float* g_sumexp_m1,
                        const float* grad_output, int64_t gout_stride, void* grad_hidden,
                        void* grad_weight, int64_t vocab_chunk, void* workspace,
                        int64_t workspace_bytes, void* stream);

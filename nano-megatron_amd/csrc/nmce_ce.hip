@@ -42,7 +42,8 @@ constexpr int kValidateThreads = 256;
 // seen only -inf keep finite shifts and 2^(x-m) stays 0 rather than NaN.
 constexpr float kMaxFloor = -1.0e38f;
 
-// Fold K values into a running (m, s) pair, s = sum exp(x - m).
+// Fold K values into a running (m, s) pair, s = sum exp(x - m). (bf16 rows;
+// the lane's t is s - 1 afterwards, exact since s >= 1 once a value is in.)
 template <int K>
 __device__ __forceinline__ void online_fold(float& m, float& s, const float* f) {
   float cm = f[0];
@@ -61,6 +62,48 @@ __device__ __forceinline__ void online_fold(float& m, float& s, const float* f) 
   m = nm;
 }
 
+// Fold K values into a running (m, t) pair, t = sum exp(x - m) - 1 (fp32
+// rows). The terms that equal 1 -- the new maximum and its ties -- are counted
+// apart from the rest (fract leaves the others and zeroes those), so the
+// maximum's 1 never enters a rounded sum with the small terms.
+template <int K>
+__device__ __forceinline__ void fold_excess(float& m, float& t, const float* f) {
+  float cm = f[0];
+#pragma unroll
+  for (int k = 1; k < K; ++k) cm = fmaxf(cm, f[k]);
+  const float nm = fmaxf(m, cm);
+  float e[K], r[K];
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    e[k] = exp_shift(f[k], nm);
+    r[k] = __builtin_amdgcn_fractf(e[k]);
+  }
+#pragma unroll
+  for (int w = 1; w < K; w *= 2) {
+#pragma unroll
+    for (int k = 0; k + w < K; k += 2 * w) {
+      e[k] += e[k + w];
+      r[k] += r[k + w];
+    }
+  }
+  const float ones = rintf(e[0] - r[0]);  // terms equal to 1 (at most K)
+  // A new maximum: the old sum 1 + t is rescaled and this chunk brings the
+  // new 1 (left out of t) and its ties. Otherwise the chunk's terms add on.
+  t = nm > m ? fmaf(1.0f + t, exp_shift(m, nm), (ones - 1.0f) + r[0]) : t + e[0];
+  m = nm;
+}
+
+// Per-lane accumulation: exact (m, t) for fp32 rows. A bf16 row streams twice
+// as many values per byte and the forward is bound by VALU issue there: the
+// exact fold's two extra operations per value cost 13% of its time, so bf16
+// lanes keep (m, s), one rounding into s per chunk, and a confident bf16
+// token's t carries an absolute error of a few 2^-24.
+template <bool kExact, int K>
+__device__ __forceinline__ void lane_fold(float& m, float& a, const float* f) {
+  if constexpr (kExact) fold_excess<K>(m, a, f);
+  else online_fold<K>(m, a, f);
+}
+
 // Byte offset of p from the previous 16-byte boundary, in elements of T.
 template <typename T>
 __device__ __forceinline__ int64_t head_elems(const T* p, int64_t v) {
@@ -69,10 +112,12 @@ __device__ __forceinline__ int64_t head_elems(const T* p, int64_t v) {
   return h < v ? h : v;
 }
 
-// kFinal = false: per-shard statistics (out0 = row max, out1 = row exp-sum,
-//                  out2 = raw target logit or 0 when the shard does not own it).
+// kFinal = false: per-shard statistics (out0 = row max, out1 = row exp-sum
+//                  minus one, out2 = raw target logit or 0 when the shard does
+//                  not own it).
 // kFinal = true:  the shard is the whole vocabulary (TP=1), so the combine is
-//                  folded in: out0 = max, out1 = exp-sum, out2 = per-token loss.
+//                  folded in: out0 = max, out1 = exp-sum minus one, out2 =
+//                  per-token loss.
 template <typename T, bool kFinal, int kBlock = kStatsBlock, int kUnroll = kStatsUnroll>
 __global__ __launch_bounds__(kBlock) void ce_stats_kernel(
     const T* __restrict__ x, int64_t n_rows, int64_t V, int64_t ld,
@@ -81,6 +126,7 @@ __global__ __launch_bounds__(kBlock) void ce_stats_kernel(
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
   constexpr int kWaves = kBlock / 64;
+  static_assert(kWaves <= 64, "the workgroup merge puts one wave's pair per lane");
   __shared__ float sm_m[kWaves];
   __shared__ float sm_s[kWaves];
   const int tid = threadIdx.x;
@@ -94,7 +140,8 @@ __global__ __launch_bounds__(kBlock) void ce_stats_kernel(
     const int64_t body_end = head + nvec * EPV;
     const u32x4* vp = reinterpret_cast<const u32x4*>(xr + head);
 
-    float m = kMaxFloor, s = 0.0f;
+    constexpr bool kExact = sizeof(T) == 4;
+    float m = kMaxFloor, a = kExact ? -1.0f : 0.0f;  // a: t (exact) or s
     int64_t i = tid;
     for (; i + (kUnroll - 1) * kBlock < nvec; i += kUnroll * kBlock) {
       u32x4 v[kUnroll];
@@ -103,12 +150,12 @@ __global__ __launch_bounds__(kBlock) void ce_stats_kernel(
       float f[kUnroll * EPV];
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) E::unpack(v[u], f + u * EPV);
-      online_fold<kUnroll * EPV>(m, s, f);
+      lane_fold<kExact, kUnroll * EPV>(m, a, f);
     }
     for (; i < nvec; i += kBlock) {
       float f[EPV];
       E::unpack(load_stream(vp + i), f);
-      online_fold<EPV>(m, s, f);
+      lane_fold<kExact, EPV>(m, a, f);
     }
     // Scalar head (before the first 16-byte boundary) and tail elements.
     {
@@ -117,53 +164,52 @@ __global__ __launch_bounds__(kBlock) void ce_stats_kernel(
       else if (tid >= EPV && tid - EPV < V - body_end) j = body_end + (tid - EPV);
       if (j >= 0) {
         float f[1] = {E::load1(xr + j)};
-        online_fold<1>(m, s, f);
+        lane_fold<kExact, 1>(m, a, f);
       }
     }
 
     // Wave merge (DPP), then workgroup merge through LDS.
-    const float wm = wave_max(m);
-    const float ws = wave_sum(s * exp2_hw((m - wm) * kLog2e));
+    float t = kExact ? a : a - 1.0f;
+    wave_merge_excess(m, t);
     if (lane == 0) {
-      sm_m[wave] = wm;
-      sm_s[wave] = ws;
+      sm_m[wave] = m;
+      sm_s[wave] = t;
     }
     __syncthreads();
-    if (tid == 0) {
-      float M = sm_m[0];
-#pragma unroll
-      for (int w = 1; w < kWaves; ++w) M = fmaxf(M, sm_m[w]);
-      float S = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) S += sm_s[w] * exp2_hw((sm_m[w] - M) * kLog2e);
-      const int64_t lt = target[row] - vstart;
-      const float xt = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
-      out0[row] = M;
-      out1[row] = S;
-      // Same association as the reference: log(sum) - (x_t - max).
-      out2[row] = kFinal ? logf(S) - (xt - M) : xt;
+    // Workgroup merge: wave 0 takes the waves' pairs (lanes past kWaves are
+    // empty pairs) and merges them the same way, with DPP.
+    if (wave == 0) {
+      float M = lane < kWaves ? sm_m[lane] : kMaxFloor;
+      float T1 = lane < kWaves ? sm_s[lane] : -1.0f;
+      wave_merge_excess(M, T1);
+      if (lane == 0) {
+        const int64_t lt = target[row] - vstart;
+        const float xt = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
+        out0[row] = M;
+        out1[row] = T1;
+        // The reference's log(sum) - (x_t - max), with log(sum) = log1p(sum - 1).
+        out2[row] = kFinal ? log1pf(T1) - (xt - M) : xt;
+      }
     }
     __syncthreads();
   }
 }
 
 __global__ __launch_bounds__(256) void ce_combine_kernel(
-    const float* __restrict__ m, const float* __restrict__ s, const float* __restrict__ t,
+    const float* __restrict__ m, const float* __restrict__ s1, const float* __restrict__ t,
     int tp, int64_t shard_stride, int64_t n_rows, float* __restrict__ loss,
-    float* __restrict__ g_max, float* __restrict__ g_sum) {
+    float* __restrict__ g_max, float* __restrict__ g_sum1) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (row >= n_rows) return;
-  float M = m[row];
-  for (int k = 1; k < tp; ++k) M = fmaxf(M, m[k * shard_stride + row]);
-  float S = 0.0f, xt = 0.0f;
-  for (int k = 0; k < tp; ++k) {
-    S += s[k * shard_stride + row] * exp2_hw((m[k * shard_stride + row] - M) * kLog2e);
+  float M = m[row], T1 = s1[row], xt = t[row];
+  for (int k = 1; k < tp; ++k) {
+    merge_excess(M, T1, m[k * shard_stride + row], s1[k * shard_stride + row]);
     xt += t[k * shard_stride + row];
   }
-  // Same association as the reference: log(sum) - (x_t - max).
-  if (loss) loss[row] = logf(S) - (xt - M);
+  // The reference's log(sum) - (x_t - max), with log(sum) = log1p(sum - 1).
+  if (loss) loss[row] = log1pf(T1) - (xt - M);
   if (g_max) g_max[row] = M;
-  if (g_sum) g_sum[row] = S;
+  if (g_sum1) g_sum1[row] = T1;
 }
 
 // Count of targets outside [0, vocab_total) per slot of
@@ -196,17 +242,38 @@ __global__ __launch_bounds__(kValidateThreads) void validate_targets_kernel(
   }
 }
 
-// grad = (exp(x - M) / S - onehot) * g for one element; the onehot column
-// follows the reference's order: softmax first, minus one, then times g.
-__device__ __forceinline__ float target_grad(float x, float M, float S, float g) {
-  return (exp_shift(x, M) / S - 1.0f) * g;
+// The target column's gradient, (softmax - 1) * g with softmax =
+// exp(x - M) / (1 + T1). When the target is the maximum this is
+// -T1 / (1 + T1) * g, formed from T1 itself: for a confident token it keeps
+// full relative precision instead of being the difference of two numbers
+// near 1. Otherwise the maximum's own 1 is part of 1 + T1 as well as the
+// target's term, so the softmax is at most 1/2 and softmax - 1 loses nothing.
+__device__ __forceinline__ float target_grad(float x, float M, float T1, float g) {
+  const float S = 1.0f + T1;
+  return x == M ? -T1 / S * g : (exp_shift(x, M) / S - 1.0f) * g;
+}
+
+// Replace y[d] by the target column's gradient when 0 <= d < K, with px the
+// vector's first logit. The target's logit is read again from px[d] (the
+// line is in cache, and only the lanes holding a target take this path):
+// picking it out of the unpacked registers with selects is compiled into a
+// dynamically indexed array, which the compiler stages through LDS on every
+// vector.
+template <int K, typename T>
+__device__ __forceinline__ void set_target(float* y, const T* px, int64_t d, float M, float T1,
+                                           float g) {
+  if (static_cast<uint64_t>(d) < static_cast<uint64_t>(K)) {
+    const float yt = target_grad(Elem<T>::load1(px + d), M, T1, g);
+#pragma unroll
+    for (int k = 0; k < K; ++k) y[k] = (k == d) ? yt : y[k];
+  }
 }
 
 template <typename T, bool kVec, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
 __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
-    const float* __restrict__ g_sum, const float* __restrict__ gout, int64_t gstride,
+    const float* __restrict__ g_sum1, const float* __restrict__ gout, int64_t gstride,
     float gdiv) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
@@ -215,9 +282,9 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const T* xr = x + row * ld;
     T* gr = g + row * ldg;
     const float M = g_max[row];
-    const float S = g_sum[row];
+    const float T1 = g_sum1[row];
     const float go = gout[row * gstride] / gdiv;
-    const float scale = go / S;
+    const float scale = go / (1.0f + T1);
     const int64_t lt = target[row] - vstart;  // owned iff 0 <= lt < V
 
     if constexpr (kVec) {
@@ -238,12 +305,8 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
           E::unpack(v[u], f);
 #pragma unroll
           for (int k = 0; k < EPV; ++k) y[k] = exp_shift(f[k], M) * scale;
-          const int64_t d = lt_body - (i + u * kBlock) * EPV;
-          if (static_cast<uint64_t>(d) < static_cast<uint64_t>(EPV)) {
-#pragma unroll
-            for (int k = 0; k < EPV; ++k)
-              if (k == d) y[k] = target_grad(f[k], M, S, go);
-          }
+          set_target<EPV>(y, xr + head + (i + u * kBlock) * EPV, lt_body - (i + u * kBlock) * EPV,
+                          M, T1, go);
           store_stream(gp + i + u * kBlock, E::pack(y));
         }
       }
@@ -252,12 +315,7 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
         E::unpack(load_stream(vp + i), f);
 #pragma unroll
         for (int k = 0; k < EPV; ++k) y[k] = exp_shift(f[k], M) * scale;
-        const int64_t d = lt_body - i * EPV;
-        if (static_cast<uint64_t>(d) < static_cast<uint64_t>(EPV)) {
-#pragma unroll
-          for (int k = 0; k < EPV; ++k)
-            if (k == d) y[k] = target_grad(f[k], M, S, go);
-        }
+        set_target<EPV>(y, xr + head + i * EPV, lt_body - i * EPV, M, T1, go);
         store_stream(gp + i, E::pack(y));
       }
       int64_t j = -1;
@@ -265,13 +323,13 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
       else if (tid >= EPV && tid - EPV < V - body_end) j = body_end + (tid - EPV);
       if (j >= 0) {
         const float f = E::load1(xr + j);
-        E::store1(gr + j, j == lt ? target_grad(f, M, S, go)
+        E::store1(gr + j, j == lt ? target_grad(f, M, T1, go)
                                   : exp_shift(f, M) * scale);
       }
     } else {
       for (int64_t j = tid; j < V; j += kBlock) {
         const float f = E::load1(xr + j);
-        E::store1(gr + j, j == lt ? target_grad(f, M, S, go)
+        E::store1(gr + j, j == lt ? target_grad(f, M, T1, go)
                                   : exp_shift(f, M) * scale);
       }
     }
@@ -287,7 +345,7 @@ template <typename T, int kBlock = kFlatBlock, int kUnroll = kFlatUnroll>
 __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     const T* x, T* g, uint32_t n_vec, uint32_t vpr, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
-    const float* __restrict__ g_sum, const float* __restrict__ gout, int64_t gstride,
+    const float* __restrict__ g_sum1, const float* __restrict__ gout, int64_t gstride,
     float gdiv) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
@@ -310,19 +368,15 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     if (f >= n_vec) continue;
     const uint32_t row = rows[u];
     const float M = g_max[row];
-    const float S = g_sum[row];
+    const float T1 = g_sum1[row];
     const float go = gstride == 0 ? g0 : gout[row * gstride] / gdiv;
-    const float scale = go / S;
+    const float scale = go / (1.0f + T1);
     const int64_t d = target[row] - vstart - cols[u];
     float f32[EPV], y[EPV];
     E::unpack(v[u], f32);
 #pragma unroll
     for (int k = 0; k < EPV; ++k) y[k] = exp_shift(f32[k], M) * scale;
-    if (static_cast<uint64_t>(d) < static_cast<uint64_t>(EPV)) {
-#pragma unroll
-      for (int k = 0; k < EPV; ++k)
-        if (k == d) y[k] = target_grad(f32[k], M, S, go);
-    }
+    set_target<EPV>(y, x + row * ld + cols[u], d, M, T1, go);
     store_stream(reinterpret_cast<u32x4*>(g + row * ldg + cols[u]), E::pack(y));
   }
 }
@@ -411,30 +465,30 @@ int nmce_version(void) { return (1 << 16) | 0; }
 
 int nmce_ce_fwd_stats(const void* logits, int dtype, int64_t n_rows, int64_t vocab_local,
                       int64_t ld, const int64_t* target, int64_t vocab_start, float* row_max,
-                      float* row_sumexp, float* target_logit, void* stream) {
+                      float* row_sumexp_m1, float* target_logit, void* stream) {
   return launch_stats<false>(logits, dtype, n_rows, vocab_local, ld, target, vocab_start,
-                             row_max, row_sumexp, target_logit, stream);
+                             row_max, row_sumexp_m1, target_logit, stream);
 }
 
 int nmce_ce_fwd(const void* logits, int dtype, int64_t n_rows, int64_t vocab, int64_t ld,
-                const int64_t* target, float* loss, float* g_max, float* g_sumexp,
+                const int64_t* target, float* loss, float* g_max, float* g_sumexp_m1,
                 void* stream) {
-  return launch_stats<true>(logits, dtype, n_rows, vocab, ld, target, 0, g_max, g_sumexp, loss,
+  return launch_stats<true>(logits, dtype, n_rows, vocab, ld, target, 0, g_max, g_sumexp_m1, loss,
                             stream);
 }
 
-int nmce_ce_combine(const float* row_max, const float* row_sumexp, const float* target_logit,
+int nmce_ce_combine(const float* row_max, const float* row_sumexp_m1, const float* target_logit,
                     int tp, int64_t shard_stride, int64_t n_rows, float* loss, float* g_max,
-                    float* g_sumexp, void* stream) {
+                    float* g_sumexp_m1, void* stream) {
   if (tp < 1) return NMCE_EINVAL_TP;
   if (n_rows < 0 || (tp > 1 && shard_stride < n_rows)) return NMCE_EINVAL_SHAPE;
   if (n_rows == 0) return NMCE_OK;
-  if (!row_max || !row_sumexp || !target_logit) return NMCE_EINVAL_PTR;
+  if (!row_max || !row_sumexp_m1 || !target_logit) return NMCE_EINVAL_PTR;
   const int64_t blocks = (n_rows + 255) / 256;
   if (blocks > INT32_MAX) return NMCE_EINVAL_SHAPE;
   hipLaunchKernelGGL(ce_combine_kernel, dim3(static_cast<unsigned>(blocks)), dim3(256), 0,
-                     static_cast<hipStream_t>(stream), row_max, row_sumexp, target_logit, tp,
-                     shard_stride, n_rows, loss, g_max, g_sumexp);
+                     static_cast<hipStream_t>(stream), row_max, row_sumexp_m1, target_logit, tp,
+                     shard_stride, n_rows, loss, g_max, g_sumexp_m1);
   return launch_status();
 }
 
@@ -456,15 +510,15 @@ int nmce_validate_targets(const int64_t* target, int64_t n_rows, int64_t vocab_t
 
 int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab_local,
                 int64_t ld, int64_t ld_grad, const int64_t* target, int64_t vocab_start,
-                const float* g_max, const float* g_sumexp, const float* grad_output,
+                const float* g_max, const float* g_sumexp_m1, const float* grad_output,
                 int64_t gout_stride, void* stream) {
   return nmce_ce_bwd_scaled(logits, grad, dtype, n_rows, vocab_local, ld, ld_grad, target,
-                            vocab_start, g_max, g_sumexp, grad_output, gout_stride, 1.0f, stream);
+                            vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, 1.0f, stream);
 }
 
 int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows,
                        int64_t vocab_local, int64_t ld, int64_t ld_grad, const int64_t* target,
-                       int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                       int64_t vocab_start, const float* g_max, const float* g_sumexp_m1,
                        const float* grad_output, int64_t gout_stride, float gout_div,
                        void* stream) {
   if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
@@ -472,7 +526,7 @@ int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows
       gout_stride < 0 || !(gout_div > 0.0f))
     return NMCE_EINVAL_SHAPE;
   if (n_rows == 0) return NMCE_OK;
-  if (!logits || !grad || !target || !g_max || !g_sumexp || !grad_output) return NMCE_EINVAL_PTR;
+  if (!logits || !grad || !target || !g_max || !g_sumexp_m1 || !grad_output) return NMCE_EINVAL_PTR;
   if (grad == logits && ld_grad != ld) return NMCE_EINVAL_SHAPE;
   const size_t es = dtype == NMCE_F32 ? 4 : 2;
   const uintptr_t px = reinterpret_cast<uintptr_t>(logits), pg = reinterpret_cast<uintptr_t>(grad);
@@ -496,19 +550,19 @@ int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows
       hipLaunchKernelGGL((ce_bwd_flat_kernel<float>), fgrid, dim3(kFlatBlock), 0, st,
                          static_cast<const float*>(logits), static_cast<float*>(grad),
                          static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
-                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride, gout_div);
+                         target, vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div);
     else
       hipLaunchKernelGGL((ce_bwd_flat_kernel<uint16_t>), fgrid, dim3(kFlatBlock), 0, st,
                          static_cast<const uint16_t*>(logits), static_cast<uint16_t*>(grad),
                          static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
-                         target, vocab_start, g_max, g_sumexp, grad_output, gout_stride, gout_div);
+                         target, vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div);
     return launch_status();
   }
   const dim3 grid(grid_for_rows(n_rows)), block(kBwdBlock);
 #define NMCE_BWD_LAUNCH(T, V)                                                              \
   hipLaunchKernelGGL((ce_bwd_kernel<T, V>), grid, block, 0, st, static_cast<const T*>(logits), \
                      static_cast<T*>(grad), n_rows, vocab_local, ld, ld_grad, target,           \
-                     vocab_start, g_max, g_sumexp, grad_output, gout_stride, gout_div)
+                     vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div)
   if (dtype == NMCE_F32) {
     if (vec) NMCE_BWD_LAUNCH(float, true); else NMCE_BWD_LAUNCH(float, false);
   } else {

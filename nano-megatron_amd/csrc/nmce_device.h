@@ -32,6 +32,26 @@ __device__ __forceinline__ float exp2_hw(float x) { return __builtin_amdgcn_exp2
 // token's loss.)
 __device__ __forceinline__ float exp_shift(float x, float m) { return exp2_hw((x - m) * kLog2e); }
 
+// ---- row statistics as (max, sum - 1) --------------------------------------
+// A set of values x_j is summarised by m = max_j x_j and
+// t = sum_j exp(x_j - m) - 1: the maximum's own term, exactly 1, is left out.
+// For a confident token every other term is small, and t keeps its relative
+// precision where the fp32 sum 1 + t would round it to a multiple of 2^-24;
+// the loss log1p(t) - (x_t - m) and the target's gradient
+// (expm1(x_t - m) - t) / (1 + t) * g then carry no cancellation. An empty set
+// is (any floor, -1).
+
+// Merge (m2, t2) into (m, t): the smaller maximum's whole sum, 1 + t, is
+// rescaled onto the larger and added to its t.
+__device__ __forceinline__ void merge_excess(float& m, float& t, float m2, float t2) {
+  const bool keep = m >= m2;
+  const float big_t = keep ? t : t2;
+  const float small_m = keep ? m2 : m;
+  const float small_t = keep ? t2 : t;
+  m = keep ? m : m2;
+  t = fmaf(1.0f + small_t, exp_shift(small_m, m), big_t);
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
@@ -123,6 +143,19 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<0x142, 0xa>(kNegHuge, v));
   v = fmaxf(v, dpp_f<0x143, 0xc>(kNegHuge, v));
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
+}
+
+// (m, t) of the whole wave, returned uniformly; every lane must be active.
+// Lanes at the wave's maximum add their t and their 1; the result leaves
+// out one of those 1s. Every added term is non-negative (or the -1 of an
+// empty lane at the maximum, which only happens when every lane is empty).
+__device__ __forceinline__ void wave_merge_excess(float& m, float& t) {
+  const float wm = wave_max(m);
+  const bool top = m == wm;
+  const float y = top ? t : (1.0f + t) * exp_shift(m, wm);
+  const int ones = __popcll(__ballot(top));
+  t = wave_sum(y) + static_cast<float>(ones - 1);
+  m = wm;
 }
 
 }  // namespace nmce

@@ -285,14 +285,14 @@ __device__ __forceinline__ int acc_row(int fm, int e, int fhalf) {
 
 // ---------------------------------------------------------------------------
 // Forward: Z^T tile -> per (128-row vocabulary block, token) partial stats.
-//   pmax[b*N + t], psum[b*N + t] = max and sum exp(z - max) over the block's
-//   valid rows; ptgt[b*N + t] = z of the target row if it lies in the block,
-//   else 0. (cross_entropy.py:21, :28-36, :40-41 restricted to the block.)
+//   pmax[b*N + t], psum1[b*N + t] = max and sum exp(z - max) - 1 over the
+//   block's valid rows; ptgt[b*N + t] = z of the target row if it lies in the
+//   block, else 0. (cross_entropy.py:21, :28-36, :40-41 restricted to the block.)
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
     const uint16_t* __restrict__ W, const uint16_t* __restrict__ X, int64_t V, int64_t N,
     int64_t H, const int64_t* __restrict__ target, int64_t vstart, float* __restrict__ pmax,
-    float* __restrict__ psum, float* __restrict__ ptgt) {
+    float* __restrict__ psum1, float* __restrict__ ptgt) {
   extern __shared__ __align__(16) char lds[];
   const int tiles_m = static_cast<int>((V + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
@@ -334,73 +334,74 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
         pick = (r == tl) ? z : pick;
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    float s = 0.0f;
+    // sum exp(z - mx) - 1 with the terms equal to 1 (the maximum and its
+    // ties) counted apart: fract zeroes exactly those, so the maximum's 1
+    // never enters a rounded sum with the small terms.
+    float se = 0.0f, sr = 0.0f;
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm)
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = acc_row(fm, e, fhalf);
         const float p = exp_shift(acc.c[fm][fn][e], mx);
-        s += (r < valid_rows) ? p : 0.0f;
+        const bool ok = r < valid_rows;
+        se += ok ? p : 0.0f;
+        sr += ok ? __builtin_amdgcn_fractf(p) : 0.0f;
       }
-    s += __shfl_xor(s, 32);
+    se += __shfl_xor(se, 32);
+    sr += __shfl_xor(sr, 32);
     pick += __shfl_xor(pick, 32);
+    const float ones = rintf(se - sr);  // at least the maximum's own 1
     if (fhalf == 0 && tok_ok) {
       pmax[blk * N + tok] = mx;
-      psum[blk * N + tok] = s;
+      psum1[blk * N + tok] = (ones - 1.0f) + sr;
       ptgt[blk * N + tok] = pick;
     }
   }
 }
 
 // Merge the partial statistics of nb vocabulary blocks into shard statistics:
-// max, sum exp relative to it, and the target logit (0 when not in the shard).
-// A workgroup takes 16 tokens; 16 slices of its threads stride over the
-// blocks with an online (max, sum) each, then merge through LDS.
+// max, sum exp relative to it minus one, and the target logit (0 when not in
+// the shard). A workgroup takes 16 tokens; 16 slices of its threads stride
+// over the blocks with a running (max, sum - 1) each, then merge through LDS.
 constexpr int kRedTokens = 16;
 constexpr int kRedSlices = 16;
 
 __global__ __launch_bounds__(kRedTokens * kRedSlices) void lmhead_reduce_partials_kernel(
-    const float* __restrict__ pmax, const float* __restrict__ psum,
+    const float* __restrict__ pmax, const float* __restrict__ psum1,
     const float* __restrict__ ptgt, int64_t nb, int64_t N, float* __restrict__ row_max,
-    float* __restrict__ row_sumexp, float* __restrict__ target_logit) {
+    float* __restrict__ row_sumexp_m1, float* __restrict__ target_logit) {
   __shared__ float sm[kRedSlices][kRedTokens], ss[kRedSlices][kRedTokens],
       st[kRedSlices][kRedTokens];
   const int tl = threadIdx.x % kRedTokens;
   const int slice = threadIdx.x / kRedTokens;
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kRedTokens + tl;
-  float m = kMaxFloorL, sum = 0.0f, tg = 0.0f;
+  float m = kMaxFloorL, sum1 = -1.0f, tg = 0.0f;
   if (t < N) {
     for (int64_t b = slice; b < nb; b += kRedSlices) {
-      const float bm = pmax[b * N + t];
-      const float bs = psum[b * N + t];
+      merge_excess(m, sum1, pmax[b * N + t], psum1[b * N + t]);
       tg += ptgt[b * N + t];
-      const float nm = fmaxf(m, bm);
-      sum = sum * exp2_hw((m - nm) * kLog2e) + bs * exp2_hw((bm - nm) * kLog2e);
-      m = nm;
     }
   }
   sm[slice][tl] = m;
-  ss[slice][tl] = sum;
+  ss[slice][tl] = sum1;
   st[slice][tl] = tg;
   __syncthreads();
   if (slice == 0 && t < N) {
-    float gm = kMaxFloorL;
-    for (int k = 0; k < kRedSlices; ++k) gm = fmaxf(gm, sm[k][tl]);
-    float gs = 0.0f, gt = 0.0f;
-    for (int k = 0; k < kRedSlices; ++k) {
-      gs = fmaf(ss[k][tl], exp2_hw((sm[k][tl] - gm) * kLog2e), gs);
+    float gm = sm[0][tl], gs = ss[0][tl], gt = st[0][tl];
+    for (int k = 1; k < kRedSlices; ++k) {
+      merge_excess(gm, gs, sm[k][tl], ss[k][tl]);
       gt += st[k][tl];
     }
     row_max[t] = gm;
-    row_sumexp[t] = gs;
+    row_sumexp_m1[t] = gs;
     target_logit[t] = gt;
   }
 }
 
 // ---------------------------------------------------------------------------
 // Backward, step 1: recompute a chunk of Z^T and write
-//   dZ[v, t] = (exp(z - gmax[t]) / gsum[t] - [v == target[t]]) * g[t]
+//   dZ[v, t] = (exp(z - gmax[t]) / (1 + gsum1[t]) - [v == target[t]]) * g[t]
 // (cross_entropy.py:53-65) as bf16 into dzt[v * ldt + t] and dz[t * ldz + v].
 // Rows v >= Mvalid and tokens t >= N are written as 0 (they pad the K extents
 // of the two GEMMs that follow). The tile goes through LDS so that both
@@ -409,7 +410,7 @@ __global__ __launch_bounds__(kRedTokens * kRedSlices) void lmhead_reduce_partial
 __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
     const uint16_t* __restrict__ Wc, const uint16_t* __restrict__ X, int64_t Mvalid,
     int64_t Mpad, int64_t N, int64_t H, const int64_t* __restrict__ target, int64_t vfirst,
-    const float* __restrict__ gmax, const float* __restrict__ gsum,
+    const float* __restrict__ gmax, const float* __restrict__ gsum1,
     const float* __restrict__ gout, int64_t gout_stride, uint16_t* __restrict__ dzt,
     int64_t ldt, uint16_t* __restrict__ dz, int64_t ldz) {
   extern __shared__ __align__(16) char lds[];
@@ -442,25 +443,26 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
     const int tloc = wn * kWaveN + 32 * fn + (lane & 31);
     const int64_t tok = n0 + tloc;
     const bool tok_ok = tok < N;
-    float M = 0.0f, scale = 0.0f, g = 0.0f, S = 1.0f;
+    float M = 0.0f, scale = 0.0f, g = 0.0f, T1 = 0.0f;
     int tl = -1;  // target row within this wave's rows, or -1
     if (tok_ok) {
       g = gout[tok * gout_stride];
-      S = gsum[tok];
+      T1 = gsum1[tok];
       M = gmax[tok];
-      scale = g / S;
+      scale = g / (1.0f + T1);
       const int64_t t = target[tok] - vfirst - vrow0;
       tl = (t >= 0 && t < valid_rows) ? static_cast<int>(t) : -1;
     }
-    // The target row follows the reference's order, (softmax - 1) * g
-    // (cross_entropy.py:58-64): when its softmax is close to 1 the difference
-    // keeps its relative accuracy, and it is exactly 0 when the softmax is 1.
+    // The target row, (softmax - 1) * g (cross_entropy.py:58-64): when the
+    // target is the maximum, -T1 / (1 + T1) * g from T1 itself (no
+    // cancellation for a confident token, exactly 0 when T1 = 0); otherwise
+    // its softmax is at most 1/2 and the plain form loses nothing.
     float zt = 0.0f;
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm)
 #pragma unroll
       for (int e = 0; e < 16; ++e) zt = (acc_row(fm, e, fhalf) == tl) ? acc.c[fm][fn][e] : zt;
-    const float dt = (exp_shift(zt, M) / S - 1.0f) * g;
+    const float dt = zt == M ? -T1 / (1.0f + T1) * g : (exp_shift(zt, M) / (1.0f + T1) - 1.0f) * g;
 #pragma unroll
     for (int fm = 0; fm < kFM; ++fm) {
       float d[16];
@@ -726,7 +728,7 @@ int64_t nmce_lmhead_ce_bwd_workspace_bytes(int64_t n_rows, int64_t hidden, int64
 
 int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, int64_t n_rows,
                              int64_t hidden_size, int64_t vocab_local, const int64_t* target,
-                             int64_t vocab_start, float* row_max, float* row_sumexp,
+                             int64_t vocab_start, float* row_max, float* row_sumexp_m1,
                              float* target_logit, void* workspace, int64_t workspace_bytes,
                              void* stream) {
   if (dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
@@ -735,7 +737,7 @@ int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, 
   if (n_rows == 0) return NMCE_OK;
   if (!operand_ok(hidden, hidden_size) || !operand_ok(weight, hidden_size))
     return NMCE_EINVAL_ALIGN;
-  if (!target || !row_max || !row_sumexp || !target_logit) return NMCE_EINVAL_PTR;
+  if (!target || !row_max || !row_sumexp_m1 || !target_logit) return NMCE_EINVAL_PTR;
   if (n_rows > (int64_t{1} << 30) || vocab_local > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
   const int64_t need = nmce_lmhead_ce_fwd_workspace_bytes(n_rows, hidden_size, vocab_local);
   if (!workspace || workspace_bytes < need || !aligned16(workspace)) return NMCE_EINVAL_WORKSPACE;
@@ -744,18 +746,18 @@ int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, 
   auto s = static_cast<hipStream_t>(stream);
   const int64_t nb = fwd_partial_blocks(vocab_local);
   float* pmax = static_cast<float*>(workspace);
-  float* psum = pmax + nb * n_rows;
-  float* ptgt = psum + nb * n_rows;
+  float* psum1 = pmax + nb * n_rows;
+  float* ptgt = psum1 + nb * n_rows;
   const int64_t tiles = ((vocab_local + kBM - 1) / kBM) * ((n_rows + kBN - 1) / kBN);
   hipLaunchKernelGGL(lmhead_stats_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
                      kLdsBytes, s, static_cast<const uint16_t*>(weight),
                      static_cast<const uint16_t*>(hidden), vocab_local, n_rows, hidden_size,
-                     target, vocab_start, pmax, psum, ptgt);
+                     target, vocab_start, pmax, psum1, ptgt);
   if ((st = launch_status())) return st;
   hipLaunchKernelGGL(lmhead_reduce_partials_kernel,
                      dim3(static_cast<unsigned>((n_rows + kRedTokens - 1) / kRedTokens)),
-                     dim3(kRedTokens * kRedSlices), 0, s, pmax, psum, ptgt, nb, n_rows, row_max,
-                     row_sumexp, target_logit);
+                     dim3(kRedTokens * kRedSlices), 0, s, pmax, psum1, ptgt, nb, n_rows, row_max,
+                     row_sumexp_m1, target_logit);
   return launch_status();
 }
 
@@ -792,7 +794,7 @@ int bwd_prepare(const uint16_t* X, const uint16_t* W, int64_t n_rows, int64_t H,
 
 int bwd_dz(const uint16_t* X, const uint16_t* W, int64_t n_rows, int64_t H, int64_t V,
            const int64_t* target, int64_t vocab_start, const float* g_max,
-           const float* g_sumexp, const float* grad_output, int64_t gout_stride, int64_t c,
+           const float* g_sumexp_m1, const float* grad_output, int64_t gout_stride, int64_t c,
            const BwdLayout& L, char* ws, hipStream_t s) {
   const int64_t v0 = c * L.chunk;
   const int64_t mvalid = (V - v0) < L.chunk ? (V - v0) : L.chunk;
@@ -800,7 +802,7 @@ int bwd_dz(const uint16_t* X, const uint16_t* W, int64_t n_rows, int64_t H, int6
   const int64_t tiles = (mpad / kBM) * ((L.ldt + kBN - 1) / kBN);
   hipLaunchKernelGGL(lmhead_dz_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
                      kLdsBytes, s, W + v0 * H, X, mvalid, mpad, n_rows, H, target,
-                     vocab_start + v0, g_max, g_sumexp, grad_output, gout_stride,
+                     vocab_start + v0, g_max, g_sumexp_m1, grad_output, gout_stride,
                      reinterpret_cast<uint16_t*>(ws + L.off_dzt), L.ldt,
                      reinterpret_cast<uint16_t*>(ws + L.off_dz), L.chunk);
   return launch_status();
@@ -837,7 +839,7 @@ int nmce_lmhead_ce_bwd_prepare(const void* hidden, const void* weight, int dtype
 
 int nmce_lmhead_ce_bwd_dz(const void* hidden, const void* weight, int dtype, int64_t n_rows,
                           int64_t hidden_size, int64_t vocab_local, const int64_t* target,
-                          int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                          int64_t vocab_start, const float* g_max, const float* g_sumexp_m1,
                           const float* grad_output, int64_t gout_stride, int64_t vocab_chunk,
                           int64_t chunk_index, void* workspace, int64_t workspace_bytes,
                           void* stream) {
@@ -845,18 +847,18 @@ int nmce_lmhead_ce_bwd_dz(const void* hidden, const void* weight, int dtype, int
   int st = check_bwd_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, vocab_chunk,
                           workspace, workspace_bytes, L);
   if (st) return st;
-  if (!target || !g_max || !g_sumexp || !grad_output) return NMCE_EINVAL_PTR;
+  if (!target || !g_max || !g_sumexp_m1 || !grad_output) return NMCE_EINVAL_PTR;
   if (gout_stride < 0 || chunk_index < 0 || chunk_index >= L.n_chunks) return NMCE_EINVAL_SHAPE;
   if ((st = configure_lds())) return st;
   return bwd_dz(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight), n_rows,
-                hidden_size, vocab_local, target, vocab_start, g_max, g_sumexp, grad_output,
+                hidden_size, vocab_local, target, vocab_start, g_max, g_sumexp_m1, grad_output,
                 gout_stride, chunk_index, L, static_cast<char*>(workspace),
                 static_cast<hipStream_t>(stream));
 }
 
 int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_t n_rows,
                        int64_t hidden_size, int64_t vocab_local, const int64_t* target,
-                       int64_t vocab_start, const float* g_max, const float* g_sumexp,
+                       int64_t vocab_start, const float* g_max, const float* g_sumexp_m1,
                        const float* grad_output, int64_t gout_stride, void* grad_hidden,
                        void* grad_weight, int64_t vocab_chunk, void* workspace,
                        int64_t workspace_bytes, void* stream) {
@@ -865,7 +867,7 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
   int st = check_bwd_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, vocab_chunk,
                           workspace, workspace_bytes, L);
   if (st) return st;
-  if (!target || !g_max || !g_sumexp || !grad_output || !grad_hidden || !grad_weight)
+  if (!target || !g_max || !g_sumexp_m1 || !grad_output || !grad_hidden || !grad_weight)
     return NMCE_EINVAL_PTR;
   if (gout_stride < 0) return NMCE_EINVAL_SHAPE;
   if ((st = configure_lds())) return st;
@@ -888,7 +890,7 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
     const int64_t mvalid = (vocab_local - v0) < L.chunk ? (vocab_local - v0) : L.chunk;
     const int64_t mpad = round_up(mvalid, kBM);
     // dZ of this chunk, both layouts.
-    if ((st = bwd_dz(X, W, n_rows, H, vocab_local, target, vocab_start, g_max, g_sumexp,
+    if ((st = bwd_dz(X, W, n_rows, H, vocab_local, target, vocab_start, g_max, g_sumexp_m1,
                      grad_output, gout_stride, c, L, ws, s)))
       return st;
     // dW rows [v0, v0 + mvalid) = dZ^T_c X  (K = tokens, padded with zeros).

@@ -189,7 +189,7 @@ class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
             ctx.weight_shape = weight.shape
             return torch.empty(target.shape, dtype=torch.float32, device=dev)
         ctx.empty = False
-        out = torch.empty((3, n), dtype=torch.float32, device=dev)  # loss, max, sumexp
+        out = torch.empty((3, n), dtype=torch.float32, device=dev)  # loss, max, sumexp - 1
         loss, row_stat = out[0], out[1:]
         local = torch.empty((3, n), dtype=torch.float32, device=dev)
         ws = _workspace(lib.nmce_lmhead_ce_fwd_workspace_bytes(n, hp, V), dev)

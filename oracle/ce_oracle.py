@@ -8,7 +8,9 @@ Follows nano_megatron/cross_entropy.py:
   target pick, :40-41 exp-sum), before any all-reduce.
 * ``combine``      -- what the three all-reduces and :45 produce from the
   per-rank values (MAX of maxima, SUM of target picks, SUM of rescaled
-  exp-sums; ``loss = log(sum) - (x_t - max)``).
+  exp-sums; ``loss = log(sum) - (x_t - max)``). Exp-sums are carried minus
+  the maximum's own 1 and the loss is ``log1p(sum - 1)``, so a confident
+  token's loss and target gradient keep their relative precision.
 * ``shard_grad``   -- backward (:53-65): softmax minus the one-hot on the
   owning rank, times grad_output.
 * ``closed_form``  -- full-vocabulary ``logsumexp(x) - x[t]`` and
@@ -22,8 +24,13 @@ Pinned by (tests/test_oracle.py):
   full-vocabulary slab; shard grads == column slices of the full grad;
 * invariants: shift invariance, full-vocab grad rows sum to 0, loss >= 0,
   constant rows give log V, V = 1 gives 0;
+* -inf logits, with a shard that is -inf across a whole row, against fp64
+  autograd through ``F.cross_entropy``;
+* confident tokens (margins 20 to 80, a tie at the maximum) against 60-digit
+  decimal arithmetic, 1e-12 relative on every loss and gradient entry;
 * planted mistakes (dropped max shift, missing mask, off-by-one offset, wrong
-  sign) fail at least one of the above.
+  sign, an all -inf shard's sum left unguarded, log(sum) and softmax - 1 by
+  subtraction) fail at least one of the above.
 
 The fused LM head + loss (nano_megatron/model.py:192 feeding
 cross_entropy.py:16-85):
@@ -47,25 +54,40 @@ from __future__ import annotations
 import numpy as np
 
 
+def _sum_without(e: np.ndarray, cols: np.ndarray) -> np.ndarray:
+    """Row sums of ``e`` with the term at ``cols[r]`` left out of row r."""
+    em = e.copy()
+    em[np.arange(e.shape[0]), cols] = 0.0
+    return em.sum(axis=1)
+
+
 def closed_form(x: np.ndarray, target: np.ndarray, grad_output=None):
     """Full-vocabulary loss and gradient in fp64.
 
     ``x``: [N, V] logits (any float dtype; upcast to fp64), ``target``: [N] ids.
     Returns ``(loss[N], grad[N, V])`` with ``grad = (softmax - onehot) * g``;
     ``grad_output`` is a scalar or [N] (default 1).
+
+    The two differences from 1 are formed as sums of the remaining terms, not
+    by subtraction: ``log(s) = log1p(s - 1)`` with ``s - 1`` the sum without
+    the maximum's own term (exactly 1), and ``softmax_t - 1 = -(s - e_t) / s``
+    with ``s - e_t`` the sum without the target's term. For a confident token
+    every other term lies below fp64's resolution near 1, where ``log(s)`` and
+    ``e_t / s - 1`` would round to 0; these forms keep the relative precision.
     """
     x = np.asarray(x, dtype=np.float64)
     t = np.asarray(target, dtype=np.int64)
     n = x.shape[0]
+    rows = np.arange(n)
     m = x.max(axis=1)
     e = np.exp(x - m[:, None])
     s = e.sum(axis=1)
-    lse = m + np.log(s)
-    loss = lse - x[np.arange(n), t]
+    s_m1 = _sum_without(e, x.argmax(axis=1))
+    loss = np.log1p(s_m1) - (x[rows, t] - m)
     g = np.ones(n) if grad_output is None else np.broadcast_to(
         np.asarray(grad_output, dtype=np.float64), (n,))
     grad = e / s[:, None]
-    grad[np.arange(n), t] -= 1.0
+    grad[rows, t] = -_sum_without(e, t) / s
     grad *= g[:, None]
     return loss, grad
 
@@ -73,45 +95,61 @@ def closed_form(x: np.ndarray, target: np.ndarray, grad_output=None):
 def shard_stats(x_shard: np.ndarray, target: np.ndarray, vocab_start: int):
     """One rank's local reductions (cross_entropy.py:21, :28-36, :40-41), fp64.
 
-    Returns ``(m, s, t)``: row max, ``sum exp(x - m)`` and the raw target
-    logit if this shard owns it (else 0.0).
+    Returns ``(m, s1, t)``: row max, ``sum exp(x - m) - 1`` (the sum without
+    the maximum's own term) and the raw target logit if this shard owns it
+    (else 0.0). A row that is -inf across the whole shard has ``s1 = -1`` (an
+    empty sum): in the reference every shard subtracts the all-reduced, finite
+    maximum first, so such a shard's terms are exp(-inf) = 0.
     """
     x = np.asarray(x_shard, dtype=np.float64)
     n, v = x.shape
     tgt = np.asarray(target, dtype=np.int64)
     m = x.max(axis=1)
-    s = np.exp(x - m[:, None]).sum(axis=1)
+    empty = np.isneginf(m)
+    e = np.exp(x - np.where(empty, 0.0, m)[:, None])
+    s1 = np.where(empty, -1.0, _sum_without(e, x.argmax(axis=1)))
     local = tgt - vocab_start
     owned = (local >= 0) & (local < v)
     t = np.where(owned, x[np.arange(n), np.clip(local, 0, v - 1)], 0.0)
-    return m, s, t
+    return m, s1, t
 
 
 def combine(stats):
-    """Merge per-shard ``(m, s, t)`` triples; returns ``(M, S, loss)``.
+    """Merge per-shard ``(m, s1, t)`` triples; returns ``(M, S1, loss)``.
 
-    M = max_k m_k; S = sum_k s_k exp(m_k - M); loss = log S - (sum_k t_k - M)
-    (the all-reduces of cross_entropy.py:23, :38, :43 and the loss of :45).
+    M = max_k m_k; S1 = sum_k (1 + s1_k) exp(m_k - M) - 1, formed without the
+    subtraction (each shard at the maximum adds s1_k + 1, one such 1 is left
+    out); loss = log1p(S1) - (sum_k t_k - M). These are the all-reduces of
+    cross_entropy.py:23, :38, :43 and the loss of :45 (log(sum) = log1p(S1)).
     """
     ms = np.stack([st[0] for st in stats])
     M = ms.max(axis=0)
-    S = sum(st[1] * np.exp(st[0] - M) for st in stats)
+    with np.errstate(invalid="ignore"):
+        terms = [np.where(st[0] == M, st[1], (1.0 + st[1]) * np.exp(st[0] - M))
+                 for st in stats]
+    n_top = sum((st[0] == M).astype(np.float64) for st in stats)
+    S1 = sum(terms) + (n_top - 1.0)
     xt = sum(st[2] for st in stats)
-    return M, S, np.log(S) - (xt - M)
+    return M, S1, np.log1p(S1) - (xt - M)
 
 
-def shard_grad(x_shard: np.ndarray, target: np.ndarray, vocab_start: int, M, S,
+def shard_grad(x_shard: np.ndarray, target: np.ndarray, vocab_start: int, M, S1,
                grad_output=None):
-    """Backward on one shard (cross_entropy.py:53-65) in fp64."""
+    """Backward on one shard (cross_entropy.py:53-65) in fp64, from the combined
+    ``(M, S1)``. The owned target column's ``softmax - 1`` is formed as
+    ``(expm1(x_t - M) - S1) / (1 + S1)``: the same value, without the
+    subtraction from 1."""
     x = np.asarray(x_shard, dtype=np.float64)
     n, v = x.shape
     g = np.ones(n) if grad_output is None else np.broadcast_to(
         np.asarray(grad_output, dtype=np.float64), (n,))
+    S = 1.0 + S1
     grad = np.exp(x - M[:, None]) / S[:, None]
     local = np.asarray(target, dtype=np.int64) - vocab_start
     owned = (local >= 0) & (local < v)
     rows = np.nonzero(owned)[0]
-    grad[rows, local[rows]] -= 1.0
+    d = x[rows, local[rows]] - M[rows]
+    grad[rows, local[rows]] = (np.expm1(d) - S1[rows]) / S[rows]
     return grad * g[:, None]
 
 
@@ -119,7 +157,7 @@ def sharded(x_full: np.ndarray, target: np.ndarray, tp: int, grad_output=None):
     """Brute-force TP emulation: slice the full slab into ``tp`` shards, run
     ``shard_stats`` on each, ``combine``, then ``shard_grad`` per shard.
 
-    Returns ``(loss, [grad_shard_0, ...], M, S)``.
+    Returns ``(loss, [grad_shard_0, ...], M, S1)``.
     """
     n, vfull = x_full.shape
     if vfull % tp:
@@ -127,9 +165,9 @@ def sharded(x_full: np.ndarray, target: np.ndarray, tp: int, grad_output=None):
     per = vfull // tp
     shards = [x_full[:, r * per:(r + 1) * per] for r in range(tp)]
     stats = [shard_stats(sh, target, r * per) for r, sh in enumerate(shards)]
-    M, S, loss = combine(stats)
-    grads = [shard_grad(sh, target, r * per, M, S, grad_output) for r, sh in enumerate(shards)]
-    return loss, grads, M, S
+    M, S1, loss = combine(stats)
+    grads = [shard_grad(sh, target, r * per, M, S1, grad_output) for r, sh in enumerate(shards)]
+    return loss, grads, M, S1
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
@@ -174,10 +212,10 @@ def lmhead_sharded(hidden: np.ndarray, weight: np.ndarray, target: np.ndarray, t
         np.asarray(grad_output, dtype=np.float64), (n,))
     zs = [X @ W[r * per:(r + 1) * per].T for r in range(tp)]
     stats = [shard_stats(zs[r], target, r * per) for r in range(tp)]
-    M, S, loss = combine(stats)
+    M, S1, loss = combine(stats)
     parts, dws = [], []
     for r in range(tp):
-        dz = shard_grad(zs[r], target, r * per, M, S, g)
+        dz = shard_grad(zs[r], target, r * per, M, S1, g)
         parts.append(dz @ W[r * per:(r + 1) * per])
         dws.append(dz.T @ X)
     return loss, parts, np.concatenate(dws, axis=0)

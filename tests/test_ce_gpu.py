@@ -131,17 +131,72 @@ def test_shard_pair_fixture(name):
         assert_bf16_close(g, gold["grad_sum"], what="bf16 grad", atol=1e-30)
 
 
+# fp32's smallest normal: softmax terms below it (exp(-120) on a +-60 row)
+# come out of the exponential as 0. That is the only absolute slack the fp32
+# checks allow: 2^-126 per entry, and per term of a sum (V * 2^-126 on a
+# loss whose sum - 1 is itself near that range).
+FP32_TINY = 2.0 ** -126
+
+
 def test_edge_rows_fixture():
     """Constant rows, a dominant logit, +-60 logits, a -inf entry, targets at
-    the first and last column."""
+    the first and last column. Against the fixture (torch's fp64
+    cross_entropy, whose own rounding is ~1e-15 absolute) with that floor, and
+    against the oracle on the same values to 1e-5 relative alone: the dominant
+    logit's loss (5.9e-12) and target gradient keep their relative precision."""
     gold = load_npz("edge_rows.npz")
     x = torch.from_numpy(gold["logits"]).to(DEV)
     t = torch.from_numpy(gold["target"]).to(DEV)
     loss, _, _, grads = run_shards([x], t)
-    # A loss of ~1e-13 (dominant logit) is only defined to fp32 rounding of
-    # log(1 + tiny): compare with an absolute floor of 1e-6.
-    assert_close_rel(loss.cpu().numpy(), gold["loss"], 1e-5, 1e-6, what="loss")
-    assert_close_rel(grads[0].cpu().numpy(), gold["grad_sum"], 1e-5, 1e-7, what="grad")
+    got_l, got_g = loss.cpu().numpy(), grads[0].cpu().numpy()
+    assert_close_rel(got_l, gold["loss"], 1e-5, 1e-14, what="loss vs fixture")
+    assert_close_rel(got_g, gold["grad_sum"], 1e-5, 1e-14, what="grad vs fixture")
+    ol, og = ce_oracle.closed_form(gold["logits"], gold["target"])
+    assert_close_rel(got_l, ol, 1e-5, FP32_TINY, what="loss vs oracle")
+    assert_close_rel(got_g, og, 1e-5, FP32_TINY, what="grad vs oracle")
+
+
+@pytest.mark.parametrize("tp", [1, 2, 3])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_confident_tokens(dtype, tp):
+    """Tokens whose target leads the row by 5 to 80 (rows of width 3 * 16768,
+    logits ~ N(0, 2^2)), with a tie at the maximum on one row and the target
+    below the maximum on another. fp32 rows: loss and every gradient entry
+    within 1e-5 relative of the oracle -- for the larger margins the loss and
+    the target's gradient are below 1e-10 and exist only through the
+    (max, sum - 1) statistics -- plus V * 2^-126 times |g| for the terms under
+    fp32's normal range (at margin 80 the loss is 7e-34, and those terms
+    matter). bf16 rows: the bf16 gradient within one ulp, the loss and the
+    target column within the derived bound on their sum - 1."""
+    from test_sweep_gpu import bf16_fold_bound, bf16_fold_floor
+    n, v = 12, 3 * 16768
+    per = v // tp
+    g = torch.Generator().manual_seed(123)
+    x = torch.randn(n, v, generator=g) * 2.0
+    t = torch.randint(0, v, (n,), generator=g)
+    margins = torch.tensor([5.0, 10, 15, 20, 25, 30, 40, 50, 60, 80, 0, -3])
+    x[torch.arange(n), t] = x.max(1).values + margins
+    x[10, (t[10] + 7) % v] = x[10, t[10]]            # tie with the target
+    x = x.to(dtype)
+    xd = x.to(DEV)
+    shards = [xd[:, r * per:(r + 1) * per] for r in range(tp)]
+    go = torch.rand(n, generator=g) + 0.5
+    loss, _, _, grads = run_shards(shards, t.to(DEV), grad_output=go)
+    ol, og, _, _ = ce_oracle.sharded(x.double().numpy(), t.numpy(), tp, go.double().numpy())
+    got_l = loss.cpu().numpy()
+    if dtype == torch.float32:
+        flush = v * FP32_TINY
+        assert_close_rel(got_l, ol, 1e-5, flush, what="confident loss")
+        for r in range(tp):
+            assert_close_rel(grads[r].cpu().numpy(), og[r], 1e-5, flush * float(go.max()),
+                             what=f"confident grad shard {r}")
+    else:
+        assert_close_rel(got_l, ol, 1e-5, bf16_fold_bound(per), what="confident bf16 loss")
+        floor = bf16_fold_floor(n, v, tp, t.numpy(), go.double().numpy())
+        for r in range(tp):
+            assert_bf16_close(grads[r].double().cpu().numpy(), og[r],
+                              what=f"confident bf16 grad shard {r}",
+                              atol=FP32_TINY * float(go.max()) + floor[:, r * per:(r + 1) * per])
 
 
 def test_c1_golden_through_dropin():
@@ -181,10 +236,19 @@ def _oracle_check(x: torch.Tensor, t: torch.Tensor, tp: int, go=None, what=""):
     xv = x.float().cpu().numpy()
     tv = t.cpu().numpy()
     gov = None if go is None else go.cpu().numpy()
-    ol, og, oM, oS = ce_oracle.sharded(xv, tv, tp, gov)
-    assert_close_rel(loss.cpu().numpy(), ol, 1e-5, 1e-6, what=f"{what} loss")
+    ol, og, oM, oS1 = ce_oracle.sharded(xv, tv, tp, gov)
+    # fp32 rows keep their sum - 1 to relative precision, so the loss is held
+    # to 1e-5 relative alone; bf16 rows carry up to ~1e-6 absolute in it
+    loss_atol = 1e-30 if x.dtype == torch.float32 else 1e-6
+    assert_close_rel(loss.cpu().numpy(), ol, 1e-5, loss_atol, what=f"{what} loss")
     assert_close_rel(gm.cpu().numpy(), oM, 0, 0, what=f"{what} row max")
-    assert_close_rel(gs.cpu().numpy(), oS, 1e-5, what=f"{what} row sumexp")
+    # the exp-sum is carried minus one: relative to itself for fp32 rows,
+    # relative to the whole sum for bf16 rows (their lanes round with the 1 in)
+    if x.dtype == torch.float32:
+        assert_close_rel(gs.cpu().numpy(), oS1, 1e-5, what=f"{what} row sumexp - 1")
+    else:
+        assert_close_rel(gs.cpu().numpy(), oS1, 0.0, 1e-5 * (1.0 + oS1),
+                         what=f"{what} row sumexp - 1")
     for r in range(tp):
         got = grads[r].float().cpu().numpy()
         if x.dtype == torch.float32:

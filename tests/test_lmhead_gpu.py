@@ -63,33 +63,15 @@ def _bf16_round(a: np.ndarray) -> np.ndarray:
     return torch.from_numpy(np.ascontiguousarray(a)).float().to(torch.bfloat16).double().numpy()
 
 
-# The target entry of dZ is (softmax - 1) * g. Computed in fp32, as the
-# reference does (cross_entropy.py:58-64), the difference carries one rounding
-# of a value near 1: up to 2^-24 |g| absolute, which is large relative to dZ
-# itself for a confident token. Four such ulps are allowed on that entry.
-CANCEL_ULPS = 4 * 2.0 ** -24
-
-
-def target_floor(n: int, v: int, t: np.ndarray, g) -> np.ndarray:
-    """[n, v] floor, ``CANCEL_ULPS * |g_t|`` at each token's target column."""
-    gv = np.broadcast_to(np.abs(np.asarray(g, dtype=np.float64)), (n,))
-    f = np.zeros((n, v))
-    f[np.arange(n), np.asarray(t)] = CANCEL_ULPS * gv
-    return f
-
-
 class GradRef:
     """Exact fp64 gradient ``a @ b`` plus the same product with ``a`` (dZ)
-    rounded to bf16, the l1 product |a| @ |b| that bounds rounding flips, and
-    ``|cancel| @ |b|``: the fp32 cancellation floor of ``a`` carried through the
-    product (zero unless ``cancel`` is given)."""
+    rounded to bf16 and the l1 product |a| @ |b| that bounds rounding flips."""
 
-    def __init__(self, a: np.ndarray, b: np.ndarray, cancel=None):
+    def __init__(self, a: np.ndarray, b: np.ndarray):
         self.exact = a @ b
         ab = _bf16_round(a)
         self.rounded = ab @ b
         self.l1 = np.abs(ab) @ np.abs(b)
-        self.floor = 0.0 if cancel is None else np.abs(cancel) @ np.abs(b)
 
 
 def fp64_reference(x, w, t, g=None):
@@ -101,20 +83,17 @@ def fp64_reference(x, w, t, g=None):
     n = X.shape[0]
     g = np.full(n, 1.0 / n) if g is None else np.asarray(g, dtype=np.float64)
     loss, dz, _, _ = ce_oracle.lmhead_closed_form(X, W, t.numpy(), g)
-    cancel = target_floor(n, W.shape[0], t.numpy(), g)
-    return loss, dz, GradRef(dz, W, cancel), GradRef(dz.T.copy(), X, cancel.T.copy())
+    return loss, dz, GradRef(dz, W), GradRef(dz.T.copy(), X)
 
 
 def check_grad(got, ref: GradRef, what, norm_tol=4e-3):
     got = np.asarray(got, dtype=np.float64)
     norm = max(np.linalg.norm(ref.exact), 1e-300)
     nrel = np.linalg.norm(got - ref.exact) / norm
-    allowed = norm_tol + np.linalg.norm(ref.floor) / norm
-    assert nrel <= allowed, f"{what}: norm-relative error {nrel:.3e} > {allowed:.3e}"
+    assert nrel <= norm_tol, f"{what}: norm-relative error {nrel:.3e} > {norm_tol:.3e}"
     # output rounding (half a bf16 ulp, <= 2^-8 relative) plus one bf16 ulp
-    # (<= 2^-7 relative) on any dZ term whose rounding flipped at a tie, plus
-    # the fp32 cancellation floor of the target entries
-    bound = 2.0 ** -8 * np.abs(ref.rounded) + 2.0 ** -7 * ref.l1 + 2.0 * ref.floor + 1e-30
+    # (<= 2^-7 relative) on any dZ term whose rounding flipped at a tie
+    bound = 2.0 ** -8 * np.abs(ref.rounded) + 2.0 ** -7 * ref.l1 + 1e-30
     bad = np.abs(got - ref.rounded) > bound
     assert not bad.any(), (f"{what}: {int(bad.sum())} elements off; first at "
                            f"{np.argwhere(bad)[0]}: {got[bad][0]} vs {ref.rounded[bad][0]}")
@@ -599,7 +578,6 @@ def _grad_ref_gpu(a: torch.Tensor, b: torch.Tensor) -> GradRef:
     ab = a.float().to(torch.bfloat16).double()
     ref.rounded = (ab @ b).cpu().numpy()
     ref.l1 = (ab.abs() @ b.abs()).cpu().numpy()
-    ref.floor = 0.0
     return ref
 
 

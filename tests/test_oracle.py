@@ -9,6 +9,11 @@ Checks, each chosen so a plausible mistake fails at least one of them:
   gradient;
 * invariants: shift invariance, full-vocab gradient rows sum to 0, loss >= 0,
   constant rows give log V, V = 1 gives loss 0 and gradient 0;
+* -inf logits, including a shard that is -inf across a whole row, against
+  fp64 autograd through ``F.cross_entropy``;
+* confident tokens (target margins 20 to 80, a tie at the maximum) against
+  60-digit decimal arithmetic, to 1e-12 relative on every entry -- which the
+  subtraction forms log(sum) and softmax - 1 fail;
 * planted mistakes: mutated copies of the oracle (missing target mask,
   off-by-one shard offset, combine without rescale, onehot with the wrong
   sign, a dropped max shift) must fail these checks.
@@ -56,10 +61,18 @@ def check_shard_pairs(sharded=O.sharded):
 
 
 def check_edge_rows(closed=O.closed_form):
+    """The fixture comes from torch's fp64 cross_entropy, which forms
+    log_softmax = x - (m + log s): each of its roundings costs up to 2^-53 |m|
+    absolute, which on the dominant-logit row (margin 30, loss 5.9e-12) is
+    1e-4 of the value. So each row's loss and gradient are compared within
+    1e-12 relative plus 2^-50 (1 + |m|) absolute; the confident-row check
+    against decimal arithmetic pins those entries to 1e-12 relative."""
     gold = load_npz("edge_rows.npz")
-    l, g = closed(gold["logits"], gold["target"])
-    assert_close_rel(l, gold["loss"], 1e-12, 1e-14, what="edge loss")
-    assert_close_rel(g, gold["grad_sum"], 1e-12, 1e-15, what="edge grad")
+    x = gold["logits"].astype(np.float64)
+    l, g = closed(x, gold["target"])
+    floor = 2.0 ** -50 * (1.0 + np.abs(x.max(axis=1)))
+    assert_close_rel(l, gold["loss"], 1e-12, floor, what="edge loss")
+    assert_close_rel(g, gold["grad_sum"], 1e-12, floor[:, None], what="edge grad")
 
 
 def check_brute_force(sharded=O.sharded, closed=O.closed_form):
@@ -72,6 +85,70 @@ def check_brute_force(sharded=O.sharded, closed=O.closed_form):
         sl, sg, _, _ = sharded(x, t, tp)
         assert_close_rel(sl, fl, 1e-12, 1e-14, what=f"tp={tp} sharded vs closed loss")
         assert_close_rel(np.concatenate(sg, 1), fg, 1e-12, 1e-15, what=f"tp={tp} grad")
+
+
+def check_neg_inf_shards(sharded=O.sharded, closed=O.closed_form):
+    """-inf logits (masked vocabulary entries), including rows where one whole
+    shard is -inf: the reference subtracts the all-reduced finite maximum on
+    every shard, so such a shard adds exactly 0 to the sum. Against fp64
+    autograd through F.cross_entropy and the closed form."""
+    rng = np.random.default_rng(5)
+    n, v, tp = 9, 12, 3
+    x = rng.normal(0, 4, (n, v))
+    t = rng.integers(4, v, n)               # targets never in shard 0
+    x[rng.random((n, v)) < 0.3] = -np.inf
+    x[np.arange(n), t] = rng.normal(0, 4, n)  # targets stay finite
+    x[:4, :4] = -np.inf                     # rows 0-3: shard 0 entirely -inf
+    xt = torch.from_numpy(x).requires_grad_(True)
+    ref = torch.nn.functional.cross_entropy(xt, torch.from_numpy(t), reduction="none")
+    ref.sum().backward()
+    fl, fg = closed(x, t)
+    assert_close_rel(fl, ref.detach().numpy(), 1e-12, 1e-14, what="-inf closed loss")
+    assert_close_rel(fg, xt.grad.numpy(), 1e-12, 1e-15, what="-inf closed grad")
+    sl, sg, _, _ = sharded(x, t, tp)
+    assert_close_rel(sl, fl, 1e-12, 1e-14, what="-inf sharded loss")
+    assert_close_rel(np.concatenate(sg, 1), fg, 1e-12, 1e-15, what="-inf sharded grad")
+
+
+def _decimal_reference(x: np.ndarray, t: np.ndarray):
+    """Loss and gradient (g = 1) of each row in 60-digit decimal arithmetic,
+    straight from the definitions: loss = ln(sum_j e^(x_j)) - x_t,
+    grad_j = e^(x_j) / sum - [j == t]. The fp64 inputs convert exactly."""
+    from decimal import Decimal, localcontext
+    loss = np.empty(x.shape[0])
+    grad = np.empty(x.shape)
+    with localcontext() as ctx:
+        ctx.prec = 60
+        for r in range(x.shape[0]):
+            ex = [Decimal(float(v)).exp() for v in x[r]]
+            s = sum(ex)
+            loss[r] = float(s.ln() - Decimal(float(x[r, t[r]])))
+            for j in range(x.shape[1]):
+                grad[r, j] = float(ex[j] / s - (1 if j == t[r] else 0))
+    return loss, grad
+
+
+def check_confident_rows(sharded=O.sharded, closed=O.closed_form):
+    """Tokens whose target leads by 20 to 80: every other softmax term is below
+    fp64's resolution near 1 for the larger margins, so loss = log(sum) and
+    softmax_t - 1 are differences that fp64 rounds to 0. Each value must hold
+    its relative precision against decimal arithmetic: 1e-12 relative on every
+    loss and gradient entry (the non-target entries and the target entry
+    alike), for the closed form and the tp = 2 and 3 sharded forms."""
+    rng = np.random.default_rng(11)
+    n, v = 6, 12
+    x = rng.normal(0, 2, (n, v))
+    t = np.array([0, 3, 5, 7, 11, 4])
+    x[np.arange(n), t] += np.array([20.0, 30.0, 40.0, 45.0, 60.0, 80.0])
+    x[5, 9] = x[5, 4]                      # a tie at the maximum with the target
+    dl, dg = _decimal_reference(x, t)
+    fl, fg = closed(x, t)
+    assert_close_rel(fl, dl, 1e-12, what="confident closed loss")
+    assert_close_rel(fg, dg, 1e-12, what="confident closed grad")
+    for tp in (2, 3):
+        sl, sg, _, _ = sharded(x, t, tp)
+        assert_close_rel(sl, dl, 1e-12, what=f"confident tp={tp} loss")
+        assert_close_rel(np.concatenate(sg, 1), dg, 1e-12, what=f"confident tp={tp} grad")
 
 
 # ------------------------------------------------------------------- the tests
@@ -91,6 +168,14 @@ def test_oracle_edge_rows_golden():
 
 def test_oracle_brute_force_sharding():
     check_brute_force()
+
+
+def test_oracle_neg_inf_shards():
+    check_neg_inf_shards()
+
+
+def test_oracle_confident_rows():
+    check_confident_rows()
 
 
 def test_oracle_c1_golden():
@@ -155,12 +240,21 @@ def test_restatement_matches_golden():
 
 
 def _mut_stats_no_mask(x_shard, target, vocab_start):
+    m, s1, _ = O.shard_stats(x_shard, target, vocab_start)
+    x = np.asarray(x_shard, dtype=np.float64)
+    local = np.clip(np.asarray(target) - vocab_start, 0, x.shape[1] - 1)
+    return m, s1, x[np.arange(x.shape[0]), local]  # forgets to zero unowned picks
+
+
+def _mut_stats_unguarded(x_shard, target, vocab_start):
     x = np.asarray(x_shard, dtype=np.float64)
     n, v = x.shape
     m = x.max(1)
-    s = np.exp(x - m[:, None]).sum(1)
-    local = np.clip(np.asarray(target) - vocab_start, 0, v - 1)
-    return m, s, x[np.arange(n), local]  # forgets to zero unowned picks
+    with np.errstate(invalid="ignore"):
+        s1 = np.exp(x - m[:, None]).sum(1) - 1.0  # an all -inf row gives nan
+    local = np.asarray(target) - vocab_start
+    owned = (local >= 0) & (local < v)
+    return m, s1, np.where(owned, x[np.arange(n), np.clip(local, 0, v - 1)], 0.0)
 
 
 def _mut_stats_offset(x_shard, target, vocab_start):
@@ -169,9 +263,9 @@ def _mut_stats_offset(x_shard, target, vocab_start):
 
 def _mut_combine_no_rescale(stats):
     M = np.stack([st[0] for st in stats]).max(0)
-    S = sum(st[1] for st in stats)
+    S1 = sum(1.0 + st[1] for st in stats) - 1.0  # shard sums added unscaled
     xt = sum(st[2] for st in stats)
-    return M, S, np.log(S) - (xt - M)
+    return M, S1, np.log1p(S1) - (xt - M)
 
 
 def _sharded_with(stats_fn=O.shard_stats, combine_fn=O.combine, grad_fn=O.shard_grad):
@@ -180,14 +274,14 @@ def _sharded_with(stats_fn=O.shard_stats, combine_fn=O.combine, grad_fn=O.shard_
         per = vfull // tp
         shards = [x_full[:, r * per:(r + 1) * per] for r in range(tp)]
         stats = [stats_fn(sh, target, r * per) for r, sh in enumerate(shards)]
-        M, S, loss = combine_fn(stats)
-        grads = [grad_fn(sh, target, r * per, M, S, grad_output) for r, sh in enumerate(shards)]
-        return loss, grads, M, S
+        M, S1, loss = combine_fn(stats)
+        grads = [grad_fn(sh, target, r * per, M, S1, grad_output) for r, sh in enumerate(shards)]
+        return loss, grads, M, S1
     return run
 
 
-def _mut_grad_sign(x_shard, target, vocab_start, M, S, grad_output=None):
-    g = O.shard_grad(x_shard, target, vocab_start, M, S, None)
+def _mut_grad_sign(x_shard, target, vocab_start, M, S1, grad_output=None):
+    g = O.shard_grad(x_shard, target, vocab_start, M, S1, None)
     local = np.asarray(target) - vocab_start
     owned = (local >= 0) & (local < g.shape[1])
     rows = np.nonzero(owned)[0]
@@ -207,11 +301,43 @@ def _mut_closed_no_shift(x, target, grad_output=None):
     return loss.astype(np.float64), g.astype(np.float64) * go
 
 
+def _mut_closed_subtracting(x, target, grad_output=None):
+    x = np.asarray(x, dtype=np.float64)
+    rows = np.arange(x.shape[0])
+    m = x.max(1)
+    e = np.exp(x - m[:, None])
+    s = e.sum(1)
+    loss = np.log(s) - (x[rows, target] - m)   # log of a sum that rounded to 1
+    g = e / s[:, None]
+    g[rows, target] -= 1.0                     # softmax - 1 by subtraction
+    go = 1.0 if grad_output is None else grad_output
+    return loss, g * go
+
+
+def _mut_grad_subtracting(x_shard, target, vocab_start, M, S1, grad_output=None):
+    x = np.asarray(x_shard, dtype=np.float64)
+    g = np.exp(x - M[:, None]) / (1.0 + S1)[:, None]
+    local = np.asarray(target) - vocab_start
+    owned = (local >= 0) & (local < x.shape[1])
+    rows = np.nonzero(owned)[0]
+    g[rows, local[rows]] -= 1.0
+    go = 1.0 if grad_output is None else np.asarray(grad_output)
+    return g * (go if np.ndim(go) == 0 else go[:, None])
+
+
+def test_planted_subtractions_are_caught():
+    with pytest.raises(AssertionError):
+        check_confident_rows(closed=_mut_closed_subtracting)
+    with pytest.raises(AssertionError):
+        check_confident_rows(sharded=_sharded_with(grad_fn=_mut_grad_subtracting))
+
+
 @pytest.mark.parametrize("mutant,check", [
     (_sharded_with(stats_fn=_mut_stats_no_mask), check_tp_math),
     (_sharded_with(stats_fn=_mut_stats_offset), check_shard_pairs),
     (_sharded_with(combine_fn=_mut_combine_no_rescale), check_brute_force),
     (_sharded_with(grad_fn=_mut_grad_sign), check_shard_pairs),
+    (_sharded_with(stats_fn=_mut_stats_unguarded), check_neg_inf_shards),
 ])
 def test_planted_mistakes_in_sharding_are_caught(mutant, check):
     with pytest.raises(AssertionError):
