@@ -12,8 +12,11 @@ Differences from the reference, all deliberate:
   in the logits dtype.
 * Nothing of size ``[tokens, vocab]`` is kept between forward and backward:
   the reference saves the fp32 softmax (:48-49); this keeps two floats per
-  token (row max, row exp-sum) and recomputes the softmax in backward from the
-  logits.
+  token (row max, row exp-sum minus one) and recomputes the softmax in
+  backward from the logits. The exp-sum leaves out the maximum's own term
+  (exactly 1), so a confident token's loss log1p(sum - 1) and target gradient
+  -(sum - 1)/sum * g keep their relative precision; the reference's log(sum)
+  and softmax - 1 give the same values up to fp32 cancellation near 1.
 * By default the gradient is written **in place** into the logits storage
   when the logits are a non-leaf tensor (as at model.py:277-281, where they
   come straight from the LM-head matmul, which does not save them). Pass
@@ -208,7 +211,7 @@ def _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, 
         tgt = tgt.contiguous()
 
     dcode = _lib.dtype_code(rows.dtype)
-    # out[0] = per-token loss, out[1] = global row max, out[2] = global exp-sum
+    # out[0] = per-token loss, out[1] = global row max, out[2] = global exp-sum - 1
     out = torch.empty((3, n), dtype=torch.float32, device=dev)
     loss, row_stat = out[0], out[1:]
     if world_size == 1:
