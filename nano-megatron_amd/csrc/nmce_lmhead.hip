@@ -343,10 +343,9 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = acc_row(fm, e, fhalf);
-        const float p = exp_shift(acc.c[fm][fn][e], mx);
-        const bool ok = r < valid_rows;
-        se += ok ? p : 0.0f;
-        sr += ok ? __builtin_amdgcn_fractf(p) : 0.0f;
+        const float p = r < valid_rows ? exp_shift(acc.c[fm][fn][e], mx) : 0.0f;
+        se += p;
+        sr += __builtin_amdgcn_fractf(p);
       }
     se += __shfl_xor(se, 32);
     sr += __shfl_xor(sr, 32);
