@@ -582,3 +582,74 @@ def test_wrapper_mean_backward_is_bit_identical(dtype, inplace):
     assert torch.equal(l1, l2), (l1.item(), l2.item())
     assert torch.equal(g1.view(torch.int16) if dtype == torch.bfloat16 else g1,
                        g2.view(torch.int16) if dtype == torch.bfloat16 else g2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_empty_batch(dtype):
+    """Zero tokens, handled as the reference's torch ops handle them: the
+    per-token loss is an empty [0, s] tensor, the mean is torch's mean of
+    nothing (NaN), and the backward returns an empty gradient of the logits'
+    shape and dtype."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    x = torch.zeros(0, 16, 1000, dtype=dtype, device=DEV, requires_grad=True)
+    t = torch.zeros(0, 16, dtype=torch.int64, device=DEV)
+    per_token = nmce._VocabParallelCrossEntropy.apply(x, t, 0, 1000, None, 1)
+    assert per_token.shape == (0, 16) and per_token.dtype == torch.float32
+    per_token.sum().backward()
+    assert x.grad.shape == x.shape and x.grad.dtype == dtype
+    x.grad = None
+    loss = nmce.vocab_parallel_cross_entropy(x, t, 0, 1000, ctx)
+    want = torch.zeros(0, device=DEV).mean()  # torch's mean of an empty tensor
+    assert loss.dim() == 0 and torch.isnan(loss) and torch.isnan(want)
+    loss.backward()
+    assert x.grad.shape == x.shape
+
+
+def test_slab_at_the_flat_kernel_limit():
+    """Maximum sizes: a bf16 slab of 2^21 rows x 8192 (32 GiB, 2^34 elements)
+    with its gradient out of place (another 32 GiB). Every row offset past
+    2^31 elements is exercised, and the backward's two paths meet at their
+    boundary: 2^21 - 1 rows hold 2^31 - 1024 vectors and take the flat kernel
+    (it numbers vectors in 32 bits); all 2^21 rows hold 2^31 and take the
+    row kernel. On the shared rows the two gradients must be identical, and
+    sampled rows -- the first, the last, and those on either side of the
+    2^31-element and 2^31-vector offsets -- must match the oracle."""
+    from nmce import _lib as L
+    lib = L.load()
+    free, _ = torch.cuda.mem_get_info()
+    if free < 70 * 2 ** 30:
+        pytest.skip(f"needs 70 GiB of free device memory, {free / 2 ** 30:.0f} GiB free")
+    n, v = 2 ** 21, 8192
+    g = torch.Generator(device=DEV).manual_seed(17)
+    x = torch.empty((n, v), dtype=torch.bfloat16, device=DEV)
+    for a in range(0, n, 2 ** 15):
+        x[a:a + 2 ** 15] = torch.randn((2 ** 15, v), generator=g, device=DEV) * 1.5
+    t = torch.randint(0, v, (n,), generator=g, device=DEV)
+    stream = L.stream_handle(torch.device(DEV))
+    code = L.dtype_code(torch.bfloat16)
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    L.check(lib.nmce_ce_fwd(x.data_ptr(), code, n, v, v, t.data_ptr(), out[0].data_ptr(),
+                            out[1].data_ptr(), out[2].data_ptr(), stream), "fwd")
+    one = torch.ones(1, dtype=torch.float32, device=DEV)
+    grad = torch.empty_like(x)
+    # rows [0, n-1): the flat kernel
+    L.check(lib.nmce_ce_bwd(x.data_ptr(), grad.data_ptr(), code, n - 1, v, v, v, t.data_ptr(), 0,
+                            out[1].data_ptr(), out[2].data_ptr(), one.data_ptr(), 0, stream),
+            "bwd flat")
+    torch.cuda.synchronize()
+    rows = torch.tensor([0, 1, 2 ** 18 - 1, 2 ** 18, 2 ** 20 + 12345, n - 2], device=DEV)
+    flat_rows = grad[rows].clone()
+    # all n rows: the row kernel
+    L.check(lib.nmce_ce_bwd(x.data_ptr(), grad.data_ptr(), code, n, v, v, v, t.data_ptr(), 0,
+                            out[1].data_ptr(), out[2].data_ptr(), one.data_ptr(), 0, stream),
+            "bwd rows")
+    torch.cuda.synchronize()
+    assert torch.equal(flat_rows, grad[rows]), "flat and row kernels differ"
+    rows = torch.cat([rows, torch.tensor([n - 1], device=DEV)])
+    xs, ts = x[rows].float().cpu().numpy(), t[rows].cpu().numpy()
+    ol, og = ce_oracle.closed_form(xs, ts)
+    assert_close_rel(out[0][rows].cpu().numpy(), ol, 1e-5, 1e-6, what="loss")
+    assert_bf16_close(grad[rows].double().cpu().numpy(), og, what="grad", atol=1e-30)
+    del x, grad
+    torch.cuda.empty_cache()

@@ -653,3 +653,21 @@ def test_fused_workload(cfg):
             zmax = max(zmax, (x[i:i + 2048].float() @ w[hot].float().t()).abs().max().item())
         print(f"[fused-workload] c5 max |logit| on the scaled rows: {zmax:.1f}", flush=True)
         assert zmax > 60.0
+
+
+def test_fused_empty_batch():
+    """Zero tokens through the fused head: an empty per-token loss, the mean
+    is NaN (torch's mean of nothing), the hidden gradient is empty and the
+    weight gradient is zero (a sum over no tokens), as x @ W.t() followed by
+    the reference's loss gives."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    h = torch.zeros(0, 128, dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    w = (torch.randn(500, 128, generator=_gen(5)) * 0.02).to(torch.bfloat16).to(DEV)
+    w.requires_grad_(True)
+    t = torch.zeros(0, dtype=torch.int64, device=DEV)
+    loss = nmce.lmhead_vocab_parallel_cross_entropy(h, w, t, 0, 500, ctx)
+    assert loss.dim() == 0 and torch.isnan(loss)
+    loss.backward()
+    assert h.grad.shape == h.shape
+    assert w.grad.shape == w.shape and not w.grad.any()
