@@ -37,9 +37,9 @@ __device__ __forceinline__ float exp_shift(float x, float m) { return exp2_hw((x
 // t = sum_j exp(x_j - m) - 1: the maximum's own term, exactly 1, is left out.
 // For a confident token every other term is small, and t keeps its relative
 // precision where the fp32 sum 1 + t would round it to a multiple of 2^-24;
-// the loss log1p(t) - (x_t - m) and the target's gradient
-// (expm1(x_t - m) - t) / (1 + t) * g then carry no cancellation. An empty set
-// is (any floor, -1).
+// the loss log1p(t) - (x_t - m) and, for a target at the maximum, the
+// gradient -t / (1 + t) * g then carry no cancellation. An empty set is
+// (any floor, -1).
 
 // Merge (m2, t2) into (m, t): the smaller maximum's whole sum, 1 + t, is
 // rescaled onto the larger and added to its t.
