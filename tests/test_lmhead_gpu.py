@@ -537,18 +537,6 @@ def test_fused_head_module_fp32_tied_weight_under_autocast():
     assert loss_sp.item() == loss.item()
 
 
-def test_fused_empty_batch():
-    """No tokens: an empty per-token loss and zero gradients, nothing launched."""
-    import nmce
-    x = torch.zeros(0, 64, dtype=torch.bfloat16, device=DEV).requires_grad_(True)
-    w = torch.randn(100, 64, device=DEV).to(torch.bfloat16).requires_grad_(True)
-    t = torch.zeros(0, dtype=torch.int64, device=DEV)
-    per = nmce._LMHeadVocabParallelCrossEntropy.apply(x, w, t, 0, 100, None, 1)
-    assert per.shape == (0,)
-    per.sum().backward()
-    assert x.grad.shape == (0, 64) and float(w.grad.abs().sum()) == 0.0
-
-
 def test_dropin_rejects_bad_target():
     import nmce
     x, w, t = make_inputs(64, 64, 100, seed=1)
@@ -656,16 +644,21 @@ def test_fused_workload(cfg):
 
 
 def test_fused_empty_batch():
-    """Zero tokens through the fused head: an empty per-token loss, the mean
-    is NaN (torch's mean of nothing), the hidden gradient is empty and the
-    weight gradient is zero (a sum over no tokens), as x @ W.t() followed by
-    the reference's loss gives."""
+    """Zero tokens through the fused head, nothing launched: an empty
+    per-token loss, the mean is NaN (torch's mean of nothing), the hidden
+    gradient is empty and the weight gradient is zero (a sum over no tokens),
+    as x @ W.t() followed by the reference's loss gives."""
     import nmce
     ctx = nmce.ParallelContext.single()
     h = torch.zeros(0, 128, dtype=torch.bfloat16, device=DEV, requires_grad=True)
     w = (torch.randn(500, 128, generator=_gen(5)) * 0.02).to(torch.bfloat16).to(DEV)
     w.requires_grad_(True)
     t = torch.zeros(0, dtype=torch.int64, device=DEV)
+    per = nmce._LMHeadVocabParallelCrossEntropy.apply(h, w, t, 0, 500, None, 1)
+    assert per.shape == (0,)
+    per.sum().backward()
+    assert h.grad.shape == h.shape and not w.grad.any()
+    h.grad = w.grad = None
     loss = nmce.lmhead_vocab_parallel_cross_entropy(h, w, t, 0, 500, ctx)
     assert loss.dim() == 0 and torch.isnan(loss)
     loss.backward()
