@@ -14,6 +14,10 @@ flip per term of the product taken with dZ rounded to bf16.
 
 Unfused loss, over dtypes, ragged shard widths, padded and misaligned row
 strides, TP splits and gradient forms (tolerances in its docstring).
+
+Extreme inputs, both paths: logit scales up to 60, -inf entries and whole -inf
+shards, ties at the maximum, confident tokens, vocabularies of one or two rows
+per shard (tolerances in the docstrings).
 """
 
 from __future__ import annotations
@@ -222,3 +226,127 @@ def test_unfused_sweep(case):
         else:
             fl = floor[:, r * per:(r + 1) * per]
             assert_bf16_close(got, og[r], what=f"case {i} bf16 grad shard {r}", atol=1e-30 + fl)
+
+
+def _extreme_cases(count=40, seed=4242):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        out.append(dict(
+            i=i,
+            dtype=[torch.float32, torch.bfloat16][int(rng.integers(0, 2))],
+            n=int(rng.choice([1, 7, 64, 333])),
+            per=int(rng.choice([1, 3, 16, 100, 1025, 5000])),
+            tp=int(rng.choice([1, 2, 3])),
+            scale=float(rng.choice([0.01, 1.0, 5.0, 20.0, 60.0])),
+            kind=int(rng.integers(0, 4)),
+            per_token=bool(rng.integers(0, 2))))
+    return out
+
+
+@pytest.mark.parametrize("case", _extreme_cases(), ids=lambda c: f"case{c['i']}")
+def test_unfused_extreme_inputs(case):
+    """The unfused kernels through the C ABI on inputs at the edges of fp32:
+    logit scales 0.01 to 60; -inf entries (30% of a row, never the target),
+    which at small shard widths leave whole shards -inf on some rows; maxima
+    tied across half the row; and confident rows whose target leads by 40.
+    Against the oracle's sharded fp64 form: fp32 loss and gradients within
+    1e-5 relative (plus 2^-126 per entry and per summed term, for softmax terms
+    below fp32's normal range), bf16 as in ``test_unfused_sweep``."""
+    from _util import assert_bf16_close, assert_close_rel
+    from nmce import _lib as L
+    c = case
+    n, per, tp, dtype = c["n"], c["per"], c["tp"], c["dtype"]
+    v = per * tp
+    print(f"[extreme] case {c['i']}: {c}", flush=True)
+    lib = L.load()
+    g = torch.Generator().manual_seed(20000 + c["i"])
+    x = torch.randn(n, v, generator=g) * c["scale"]
+    t = torch.randint(0, v, (n,), generator=g)
+    if c["kind"] == 1 and v > 1:
+        mask = torch.rand(n, v, generator=g) < 0.3
+        mask[torch.arange(n), t] = False
+        x[mask] = float("-inf")
+    elif c["kind"] == 2:
+        x[:, : max(1, v // 2)] = x.max()
+    elif c["kind"] == 3:
+        x[torch.arange(n), t] += 40.0
+    x = x.to(dtype)
+    go = (torch.rand(n, generator=g) * 2.0 - 0.5) if c["per_token"] else None
+    xd, td = x.to(DEV), t.to(DEV)
+    stream = L.stream_handle(torch.device(DEV))
+    code = L.dtype_code(dtype)
+    stats = torch.empty((tp, 3, n), dtype=torch.float32, device=DEV)
+    for r in range(tp):
+        sh = xd[:, r * per:(r + 1) * per]
+        L.check(lib.nmce_ce_fwd_stats(sh.data_ptr(), code, n, per, v, td.data_ptr(), r * per,
+                                      stats[r, 0].data_ptr(), stats[r, 1].data_ptr(),
+                                      stats[r, 2].data_ptr(), stream), "stats")
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    b = stats.data_ptr()
+    L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, tp, 3 * n, n, out[0].data_ptr(),
+                                out[1].data_ptr(), out[2].data_ptr(), stream), "combine")
+    if go is None:
+        god, gs = torch.full((1,), 1.0 / n, dtype=torch.float32, device=DEV), 0
+    else:
+        god, gs = go.to(DEV), 1
+    grads = []
+    for r in range(tp):
+        sh = xd[:, r * per:(r + 1) * per]
+        gr = torch.empty((n, per), dtype=dtype, device=DEV)
+        L.check(lib.nmce_ce_bwd(sh.data_ptr(), gr.data_ptr(), code, n, per, v, per, td.data_ptr(),
+                                r * per, out[1].data_ptr(), out[2].data_ptr(), god.data_ptr(), gs,
+                                stream), "bwd")
+        grads.append(gr)
+    torch.cuda.synchronize()
+    gov = np.full(n, 1.0 / n) if go is None else go.double().numpy()
+    ol, og, _, _ = ce_oracle.sharded(x.double().numpy(), t.numpy(), tp, gov)
+    tiny = 2.0 ** -126
+    gmax = float(np.abs(gov).max())
+    if dtype == torch.float32:
+        assert_close_rel(out[0].cpu().numpy(), ol, 1e-5, v * tiny, what="loss")
+        for r in range(tp):
+            assert_close_rel(grads[r].double().cpu().numpy(), og[r], 1e-5, v * tiny * gmax,
+                             what=f"grad shard {r}")
+    else:
+        assert_close_rel(out[0].cpu().numpy(), ol, 1e-5, bf16_fold_bound(per), what="loss")
+        floor = bf16_fold_floor(n, v, tp, t.numpy(), gov)
+        for r in range(tp):
+            assert_bf16_close(grads[r].double().cpu().numpy(), og[r], what=f"bf16 grad shard {r}",
+                              atol=tiny * gmax + floor[:, r * per:(r + 1) * per])
+
+
+def _extreme_fused_cases(count=24, seed=4343):
+    rng = np.random.default_rng(seed)
+    return [dict(i=i, n=int(rng.choice([1, 64, 300])), h=int(rng.choice([64, 128, 256])),
+                 per=int(rng.choice([1, 2, 100, 300, 1024])), tp=int(rng.choice([1, 2])),
+                 wscale=float(rng.choice([0.02, 0.3, 1.0, 3.0])),
+                 chunk=int(rng.choice([0, 256])), per_token=bool(rng.integers(0, 2)))
+            for i in range(count)]
+
+
+@pytest.mark.parametrize("case", _extreme_fused_cases(), ids=lambda c: f"case{c['i']}")
+def test_fused_extreme_inputs(case):
+    """The fused path on logit scales up to ~50 (weights x 3 over H = 256),
+    vocabularies of 1 or 2 rows per shard and single tokens: the loss within
+    1e-5 relative of the fp64 closed form plus four fp32 ulps of the largest
+    |z| (the logits are fp32 sums of bf16 products), and both gradients as in
+    ``test_fused_sweep``, whose bounds carry the underflow and rounding-noise
+    terms these inputs reach."""
+    c = case
+    n, h, per, tp = c["n"], c["h"], c["per"], c["tp"]
+    v = per * tp
+    print(f"[extreme] fused case {c['i']}: {c}", flush=True)
+    g = torch.Generator().manual_seed(30000 + c["i"])
+    x = torch.randn(n, h, generator=g).to(torch.bfloat16)
+    w = (torch.randn(v, h, generator=g) * c["wscale"]).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), generator=g)
+    go = (torch.rand(n, generator=g) * 2.0 - 0.5).numpy() if c["per_token"] else None
+    loss, dx, dw = _run_shards(x, w, t, tp, c["chunk"], go)
+    X, W = x.double().numpy(), w.double().numpy()
+    gv = np.full(n, 1.0 / n) if go is None else go.astype(np.float64)
+    rl, dz, _, _ = ce_oracle.lmhead_closed_form(X, W, t.numpy(), gv)
+    zmax = float(np.abs(X @ W.T).max())
+    np.testing.assert_allclose(loss, rl, rtol=1e-5, atol=max(1e-6, 4 * 2.0 ** -24 * zmax))
+    check_grad(dx, GradRef(dz, W), f"case {c['i']} dH")
+    check_grad(dw, GradRef(dz.T.copy(), X), f"case {c['i']} dW")
