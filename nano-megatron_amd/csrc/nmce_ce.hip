@@ -1,8 +1,8 @@
 // Unfused vocabulary-parallel cross entropy for gfx950.
 //
 // Three kernels replace the ATen op chain of nano_megatron/cross_entropy.py:
-//   ce_stats_kernel   one read pass over a shard: online (max, sum exp) and the
-//                     target logit (cross_entropy.py:21, :28-36, :40-41)
+//   ce_stats_kernel   one read pass over a shard: online (max, sum exp - 1)
+//                     and the target logit (cross_entropy.py:21, :28-36, :40-41)
 //   ce_combine_kernel cross-shard merge and per-token loss, done locally
 //                     (the all-reduces at :22-23, :37-38, :42-43 and :45)
 //   ce_bwd_flat_kernel / ce_bwd_kernel
@@ -13,8 +13,9 @@
 //
 // Forward layout: one 1024-lane workgroup per row (token). A row of 50304
 // bf16 is 98 KiB; the workgroup streams it with 16-byte non-temporal loads,
-// two in flight per lane, folding them into per-lane (max, sumexp) pairs that
-// are merged with DPP inside each wave and through LDS across the 16 waves.
+// two in flight per lane, folding them into per-lane (max, sum exp - 1) pairs
+// that are merged with DPP inside each wave, then passed through LDS to wave
+// 0, which merges the 16 waves' pairs the same way.
 // Big workgroups keep fewer rows open at once (512 on 256 CUs), which keeps
 // the HBM access stream close to sequential.
 //
