@@ -472,6 +472,12 @@ def main() -> int:
                                                           # sum and grad_output in
         # the same kernel with the gradient of the mean read as one scalar
         "nmce_ce_bwd_scaled": 2 * slab_bytes + n * (8 + 8 + 4),
+        # one-pass forward + backward (TP = 1): the work of both passes, so the
+        # step's algorithmic bytes (3·V·b + 28 per token), with the logits
+        # read once on chip
+        "nmce_ce_fwd_bwd": 3 * slab_bytes + n * 28,
+        # its backward, which exits at once when the forward's gradient stands
+        "nmce_ce_bwd_scaled_unless": 8,
     }
     dominant = max(alg_bytes, key=lambda k: avg_ms.get(k, 0.0))  # one launch each per step
     achieved = alg_bytes[dominant] / (avg_ms[dominant] * 1e-3) / 1e9
@@ -498,7 +504,11 @@ def main() -> int:
             "tp": tp,
             "tp_rank": rank,
             "logits_dtype": wl["dtype"],
-            "path": "nmce.vocab_parallel_cross_entropy fwd+bwd, in-place grad, target validation",
+            "path": ("nmce.vocab_parallel_cross_entropy fwd+bwd, target validation; at TP=1 "
+                     "the one-pass kernel (logits read once, gradient to a new buffer)"
+                     if tp == 1 else
+                     "nmce.vocab_parallel_cross_entropy fwd+bwd, in-place grad, target "
+                     "validation"),
         },
         "roofline": {
             "bound": "hbm",

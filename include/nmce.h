@@ -157,6 +157,44 @@ int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows
                        int64_t gout_stride, float gout_div, void* stream);
 
 /*
+ * nmce_ce_bwd_scaled with gout_stride = 0, after nmce_ce_fwd_bwd. `assumed`
+ * (device, one float) is the upstream value that forward computed the
+ * gradient for: when grad_output[0] equals it every workgroup returns at
+ * once, leaving `grad` as written; otherwise this is nmce_ce_bwd_scaled
+ * exactly (cross_entropy.py:53-65 with the mean of :85). grad_output[0] is
+ * also written to `observed` (device, one float; may be NULL), which a
+ * caller can pass as the next forward's grad_expected.
+ */
+int nmce_ce_bwd_scaled_unless(const void* logits, void* grad, int dtype, int64_t n_rows,
+                              int64_t vocab_local, int64_t ld, int64_t ld_grad,
+                              const int64_t* target, int64_t vocab_start, const float* g_max,
+                              const float* g_sumexp_m1, const float* grad_output, float gout_div,
+                              const float* assumed, float* observed, void* stream);
+
+/*
+ * One-pass forward and backward at TP = 1 (cross_entropy.py:17-65 with the
+ * mean of :85, world_size == 1). Each row is read once and held on chip; the
+ * kernel writes g_max, g_sumexp_m1 and loss, and the gradient for the
+ * upstream value grad_expected[0] of the mean (grad_expected[0] / gout_div per
+ * token) into `grad`, a separate buffer (the row's target logit is read back
+ * from the logits); the value used goes to grad_assumed[0]. Both are device
+ * pointers to one float. Every output is bit-identical to nmce_ce_fwd
+ * followed by nmce_ce_bwd_scaled with grad_output = {grad_expected[0]} and
+ * gout_stride = 0. The backward is then nmce_ce_bwd_scaled_unless(...,
+ * assumed = grad_assumed, ...), which rewrites `grad` from the logits only
+ * when the real upstream value differs.
+ * Requirements: vocab a whole number of 16-byte vectors and at most
+ * nmce_ce_fwd_bwd_max_vocab(dtype) (65536 bf16, 32768 fp32); logits, grad
+ * and both row strides 16-byte aligned. No counterpart call in the reference,
+ * whose forward likewise computes the softmax that its backward returns.
+ */
+int64_t nmce_ce_fwd_bwd_max_vocab(int dtype);
+int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab,
+                    int64_t ld, int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
+                    float* g_sumexp_m1, const float* grad_expected, float* grad_assumed,
+                    float gout_div, void* stream);
+
+/*
  * Measurement support (no counterpart in the reference): a plain copy of
  * `bytes` (multiple of 16, both pointers 16-byte aligned) with the loss
  * kernels' access pattern -- 16-byte non-temporal loads and stores. Its HBM

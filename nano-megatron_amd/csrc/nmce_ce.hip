@@ -275,10 +275,18 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
     const float* __restrict__ g_sum1, const float* __restrict__ gout, int64_t gstride,
-    float gdiv) {
+    float gdiv, const float* __restrict__ assumed, float* __restrict__ observed) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
   const int tid = threadIdx.x;
+  // After the one-pass forward (ce_fwdbwd_kernel): record the upstream value
+  // for the next forward, and stop when it is the one this forward assumed,
+  // whose gradient is already written.
+  if (assumed) {
+    const float gv = gout[0];
+    if (observed && blockIdx.x == 0 && tid == 0) observed[0] = gv;
+    if (gv == assumed[0]) return;
+  }
   for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x) {
     const T* xr = x + row * ld;
     T* gr = g + row * ldg;
@@ -347,9 +355,14 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     const T* x, T* g, uint32_t n_vec, uint32_t vpr, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ g_max,
     const float* __restrict__ g_sum1, const float* __restrict__ gout, int64_t gstride,
-    float gdiv) {
+    float gdiv, const float* __restrict__ assumed, float* __restrict__ observed) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
+  if (assumed) {  // as in ce_bwd_kernel
+    const float gv = gout[0];
+    if (observed && blockIdx.x == 0 && threadIdx.x == 0) observed[0] = gv;
+    if (gv == assumed[0]) return;
+  }
   // With a broadcast gradient (the mean's) the per-row quotient is one value.
   const float g0 = gstride == 0 ? gout[0] / gdiv : 0.0f;
   const uint32_t base = blockIdx.x * static_cast<uint32_t>(kBlock * kUnroll) + threadIdx.x;
@@ -381,6 +394,127 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     store_stream(reinterpret_cast<u32x4*>(g + row * ldg + cols[u]), E::pack(y));
   }
 }
+
+// Forward and backward of whole-vocabulary rows (TP = 1) in one read of the
+// logits. Each workgroup walks rows blockIdx.x, + gridDim.x, ... and holds a
+// row in registers (at most kVec vectors per lane; rows 16-byte aligned, V a
+// whole number of vectors). It folds the row into (max, sum - 1) in
+// ce_stats_kernel's order and merges exactly as that kernel does, issues the
+// loads of its next row, writes the loss and the statistics, then writes the
+// gradient for the upstream value expect[0] of the mean (expect[0] / gdiv
+// per token) with ce_bwd_flat_kernel's arithmetic, from the registers; the
+// value used goes to assumed[0]. Every output is bit-identical to nmce_ce_fwd
+// followed by nmce_ce_bwd_scaled with that upstream value; the backward runs
+// only when the real value differs.
+template <typename T, int kVec, int kBlock = kStatsBlock>
+__global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
+    const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
+    const int64_t* __restrict__ target, float* __restrict__ loss, float* __restrict__ out_max,
+    float* __restrict__ out_sum1, const float* __restrict__ expect_in,
+    float* __restrict__ assumed, float gdiv) {
+  using E = Elem<T>;
+  constexpr int EPV = E::kPerVec;
+  constexpr int kWaves = kBlock / 64;
+  constexpr bool kExact = sizeof(T) == 4;
+  static_assert(kVec % 2 == 0, "vectors are folded in pairs");
+  const float expect = expect_in[0];
+  if (blockIdx.x == 0 && threadIdx.x == 0) assumed[0] = expect;
+  __shared__ float sm_m[kWaves];
+  __shared__ float sm_s[kWaves];
+  __shared__ float sm_row[2];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t nvec = V / EPV;
+  const float go = expect / gdiv;
+  u32x4 cur[kVec], nxt[kVec];
+  auto load_row = [&](int64_t r, u32x4* v) {
+    const u32x4* vp = reinterpret_cast<const u32x4*>(x + r * ld);
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) {
+      const int64_t i = tid + static_cast<int64_t>(k) * kBlock;
+      if (i < nvec) v[k] = load_stream(vp + i);
+    }
+  };
+  int64_t row = blockIdx.x;
+  if (row < n_rows) load_row(row, cur);
+  for (; row < n_rows; row += gridDim.x) {
+    const T* xr = x + row * ld;
+    // ce_stats_kernel's order: vectors k and k + 1 (kBlock apart) together
+    // while both exist, then the one left, if any.
+    float m = kMaxFloor, a = kExact ? -1.0f : 0.0f;
+    bool paired = true;
+#pragma unroll
+    for (int k = 0; k < kVec; k += 2) {
+      const int64_t i0 = tid + static_cast<int64_t>(k) * kBlock;
+      if (paired && i0 + kBlock < nvec) {
+        float f[2 * EPV];
+        E::unpack(cur[k], f);
+        E::unpack(cur[k + 1], f + EPV);
+        lane_fold<kExact, 2 * EPV>(m, a, f);
+      } else {
+        paired = false;
+        if (i0 < nvec) {
+          float f[EPV];
+          E::unpack(cur[k], f);
+          lane_fold<kExact, EPV>(m, a, f);
+        }
+      }
+    }
+    // The next row streams in while this one is merged and written.
+    const int64_t next = row + gridDim.x;
+    if (next < n_rows) load_row(next, nxt);
+    float t = kExact ? a : a - 1.0f;
+    wave_merge_excess(m, t);
+    if (lane == 0) {
+      sm_m[wave] = m;
+      sm_s[wave] = t;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      float M = lane < kWaves ? sm_m[lane] : kMaxFloor;
+      float T1 = lane < kWaves ? sm_s[lane] : -1.0f;
+      wave_merge_excess(M, T1);
+      if (lane == 0) {
+        // A target outside [0, V) (the host's check reports it after the
+        // launch) picks nothing, as in ce_stats_kernel.
+        const int64_t lt = target[row];
+        const float xt = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
+        out_max[row] = M;
+        out_sum1[row] = T1;
+        loss[row] = log1pf(T1) - (xt - M);
+        sm_row[0] = M;
+        sm_row[1] = T1;
+      }
+    }
+    __syncthreads();
+    const float M = sm_row[0];
+    const float T1 = sm_row[1];
+    const float scale = go / (1.0f + T1);
+    const int64_t lt = target[row];
+    T* gr = g + row * ldg;
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) {
+      const int64_t i = tid + static_cast<int64_t>(k) * kBlock;
+      if (i < nvec) {
+        float f[EPV], y[EPV];
+        E::unpack(cur[k], f);
+#pragma unroll
+        for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
+        set_target<EPV>(y, xr + i * EPV, lt - i * EPV, M, T1, go);
+        store_stream(reinterpret_cast<u32x4*>(gr) + i, E::pack(y));
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kVec; ++k) cur[k] = nxt[k];
+    __syncthreads();  // sm_row is rewritten for the next row
+  }
+}
+
+// Vectors per lane of ce_fwdbwd_kernel's instantiations; the smaller one that
+// holds the row is used. (16 per lane runs out of registers with the next
+// row in flight and spills.)
+constexpr int kOnePassVecs[2] = {4, 8};
 
 // Plain 16-byte streaming copy with the flat backward's access pattern
 // (non-temporal loads and stores, kFlatBlock x kFlatUnroll vectors per
@@ -517,11 +651,32 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64
                             vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, 1.0f, stream);
 }
 
-int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows,
-                       int64_t vocab_local, int64_t ld, int64_t ld_grad, const int64_t* target,
-                       int64_t vocab_start, const float* g_max, const float* g_sumexp_m1,
-                       const float* grad_output, int64_t gout_stride, float gout_div,
-                       void* stream) {
+}  // extern "C"
+
+namespace {
+// Workgroups of the one-pass kernel: two per compute unit, each walking rows.
+unsigned one_pass_grid(int64_t n_rows) {
+  static int cus[64] = {0};
+  int dev = 0;
+  int n_cu = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (cus[dev] == 0) {
+      int v = 0;
+      if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          v > 0)
+        cus[dev] = v;
+    }
+    if (cus[dev] > 0) n_cu = cus[dev];
+  }
+  const int64_t want = 2 * static_cast<int64_t>(n_cu);
+  return static_cast<unsigned>(n_rows < want ? n_rows : want);
+}
+
+int launch_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab_local,
+               int64_t ld, int64_t ld_grad, const int64_t* target, int64_t vocab_start,
+               const float* g_max, const float* g_sumexp_m1, const float* grad_output,
+               int64_t gout_stride, float gout_div, const float* assumed, float* observed,
+               void* stream) {
   if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
   if (n_rows < 0 || vocab_local < 1 || ld < vocab_local || ld_grad < vocab_local ||
       gout_stride < 0 || !(gout_div > 0.0f))
@@ -540,7 +695,8 @@ int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows
   // holds a whole number of vectors.
   const int64_t epv = 16 / static_cast<int64_t>(es);
   const int64_t vpr = vocab_local / epv;
-  const bool flat = px % 16 == 0 && pg % 16 == 0 && (ld * static_cast<int64_t>(es)) % 16 == 0 &&
+  const bool flat = !assumed && px % 16 == 0 && pg % 16 == 0 &&
+                    (ld * static_cast<int64_t>(es)) % 16 == 0 &&
                     (ld_grad * static_cast<int64_t>(es)) % 16 == 0 && vocab_local % epv == 0 &&
                     n_rows * vpr < (int64_t(1) << 31);
   if (flat) {
@@ -551,25 +707,112 @@ int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows
       hipLaunchKernelGGL((ce_bwd_flat_kernel<float>), fgrid, dim3(kFlatBlock), 0, st,
                          static_cast<const float*>(logits), static_cast<float*>(grad),
                          static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
-                         target, vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div);
+                         target, vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div,
+                         assumed, observed);
     else
       hipLaunchKernelGGL((ce_bwd_flat_kernel<uint16_t>), fgrid, dim3(kFlatBlock), 0, st,
                          static_cast<const uint16_t*>(logits), static_cast<uint16_t*>(grad),
                          static_cast<uint32_t>(n_vec), static_cast<uint32_t>(vpr), ld, ld_grad,
-                         target, vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div);
+                         target, vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div,
+                         assumed, observed);
     return launch_status();
   }
-  const dim3 grid(grid_for_rows(n_rows)), block(kBwdBlock);
+  // After the one-pass forward the backward usually exits at once: a grid of
+  // two row workgroups per compute unit makes that cost one launch, where
+  // the flat kernel's hundreds of thousands of workgroups would each start.
+  const dim3 grid(assumed ? one_pass_grid(n_rows) : grid_for_rows(n_rows)), block(kBwdBlock);
 #define NMCE_BWD_LAUNCH(T, V)                                                              \
   hipLaunchKernelGGL((ce_bwd_kernel<T, V>), grid, block, 0, st, static_cast<const T*>(logits), \
                      static_cast<T*>(grad), n_rows, vocab_local, ld, ld_grad, target,           \
-                     vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div)
+                     vocab_start, g_max, g_sumexp_m1, grad_output, gout_stride, gout_div,       \
+                     assumed, observed)
   if (dtype == NMCE_F32) {
     if (vec) NMCE_BWD_LAUNCH(float, true); else NMCE_BWD_LAUNCH(float, false);
   } else {
     if (vec) NMCE_BWD_LAUNCH(uint16_t, true); else NMCE_BWD_LAUNCH(uint16_t, false);
   }
 #undef NMCE_BWD_LAUNCH
+  return launch_status();
+}
+
+template <typename T, int kVec>
+void launch_fwdbwd(const void* logits, void* grad, int64_t n_rows, int64_t vocab, int64_t ld,
+                   int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
+                   float* g_sumexp_m1, const float* expect, float* assumed, float gout_div,
+                   hipStream_t st) {
+  hipLaunchKernelGGL((ce_fwdbwd_kernel<T, kVec>), dim3(one_pass_grid(n_rows)), dim3(kStatsBlock),
+                     0, st, static_cast<const T*>(logits), static_cast<T*>(grad), n_rows, vocab,
+                     ld, ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, gout_div);
+}
+}  // namespace
+
+extern "C" {
+
+int nmce_ce_bwd_scaled(const void* logits, void* grad, int dtype, int64_t n_rows,
+                       int64_t vocab_local, int64_t ld, int64_t ld_grad, const int64_t* target,
+                       int64_t vocab_start, const float* g_max, const float* g_sumexp_m1,
+                       const float* grad_output, int64_t gout_stride, float gout_div,
+                       void* stream) {
+  return launch_bwd(logits, grad, dtype, n_rows, vocab_local, ld, ld_grad, target, vocab_start,
+                    g_max, g_sumexp_m1, grad_output, gout_stride, gout_div, nullptr, nullptr,
+                    stream);
+}
+
+int nmce_ce_bwd_scaled_unless(const void* logits, void* grad, int dtype, int64_t n_rows,
+                              int64_t vocab_local, int64_t ld, int64_t ld_grad,
+                              const int64_t* target, int64_t vocab_start, const float* g_max,
+                              const float* g_sumexp_m1, const float* grad_output, float gout_div,
+                              const float* assumed, float* observed, void* stream) {
+  if (!assumed) return NMCE_EINVAL_PTR;
+  return launch_bwd(logits, grad, dtype, n_rows, vocab_local, ld, ld_grad, target, vocab_start,
+                    g_max, g_sumexp_m1, grad_output, 0, gout_div, assumed, observed, stream);
+}
+
+int64_t nmce_ce_fwd_bwd_max_vocab(int dtype) {
+  if (dtype != NMCE_F32 && dtype != NMCE_BF16) return 0;
+  const int64_t epv = dtype == NMCE_F32 ? 4 : 8;
+  return epv * kStatsBlock * kOnePassVecs[1];
+}
+
+int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab,
+                    int64_t ld, int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
+                    float* g_sumexp_m1, const float* grad_expected, float* grad_assumed,
+                    float gout_div, void* stream) {
+  if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
+  const int64_t es = dtype == NMCE_F32 ? 4 : 2;
+  const int64_t epv = 16 / es;
+  if (n_rows < 0 || vocab < 1 || ld < vocab || ld_grad < vocab || vocab % epv ||
+      vocab > nmce_ce_fwd_bwd_max_vocab(dtype) || !(gout_div > 0.0f))
+    return NMCE_EINVAL_SHAPE;
+  if (n_rows == 0) return NMCE_OK;
+  if (!logits || !grad || !target || !loss || !g_max || !g_sumexp_m1 || !grad_expected ||
+      !grad_assumed)
+    return NMCE_EINVAL_PTR;
+  if (grad == logits) return NMCE_EINVAL_PTR;  // the target's logit is read back from the row
+  if (reinterpret_cast<uintptr_t>(logits) % 16 || reinterpret_cast<uintptr_t>(grad) % 16 ||
+      (ld * es) % 16 || (ld_grad * es) % 16)
+    return NMCE_EINVAL_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool small = (vocab / epv + kStatsBlock - 1) / kStatsBlock <= kOnePassVecs[0];
+  if (dtype == NMCE_F32) {
+    if (small)
+      launch_fwdbwd<float, kOnePassVecs[0]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
+                                            loss, g_max, g_sumexp_m1, grad_expected, grad_assumed,
+                                            gout_div, st);
+    else
+      launch_fwdbwd<float, kOnePassVecs[1]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
+                                            loss, g_max, g_sumexp_m1, grad_expected, grad_assumed,
+                                            gout_div, st);
+  } else {
+    if (small)
+      launch_fwdbwd<uint16_t, kOnePassVecs[0]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
+                                               loss, g_max, g_sumexp_m1, grad_expected,
+                                               grad_assumed, gout_div, st);
+    else
+      launch_fwdbwd<uint16_t, kOnePassVecs[1]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
+                                               loss, g_max, g_sumexp_m1, grad_expected,
+                                               grad_assumed, gout_div, st);
+  }
   return launch_status();
 }
 

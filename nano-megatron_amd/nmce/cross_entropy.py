@@ -17,9 +17,19 @@ Differences from the reference, all deliberate:
   (exactly 1), so a confident token's loss log1p(sum - 1) and target gradient
   -(sum - 1)/sum * g keep their relative precision; the reference's log(sum)
   and softmax - 1 give the same values up to fp32 cancellation near 1.
-* By default the gradient is written **in place** into the logits storage
-  when the logits are a non-leaf tensor (as at model.py:277-281, where they
-  come straight from the LM-head matmul, which does not save them). Pass
+* The wrapper at TP = 1, on rows that fit (V a whole number of 16-byte
+  vectors, at most 65536 bf16 / 32768 fp32 columns), reads the logits once:
+  its forward also writes the gradient for the upstream value that the last
+  backward received (1.0, as for ``loss.backward()``, before the first) into
+  a new ``[tokens, vocab]`` buffer -- as the reference's forward computes the
+  softmax its backward returns -- and the backward rewrites it from the
+  logits only when its upstream value differs. A loss scaled the same way
+  every step keeps the forward's gradient from the second step on. Always
+  bit-identical to the two-pass path; ``one_pass=False`` turns it off.
+* Otherwise (TP > 1, other rows, the per-token Function, or ``inplace=True``)
+  the gradient is written **in place** into the logits storage when the
+  logits are a non-leaf tensor (as at model.py:277-281, where they come
+  straight from the LM-head matmul, which does not save them). Pass
   ``inplace=False`` to keep the logits intact; leaf tensors are never
   overwritten. The version counter of the logits is bumped after an in-place
   write, so any other autograd node that saved them fails loudly instead of
@@ -47,6 +57,23 @@ from . import _lib
 # module appends (name, start_event, end_event), both recorded on the launch
 # stream, so a caller can time each kernel inside a running workload.
 kernel_timeline: list | None = None
+
+# Per device, one float: the upstream value of the mean that the last
+# one-pass backward received (the 1.0 of ``loss.backward()`` until one has
+# run). The one-pass forward computes the gradient for it, so a training loop
+# that scales its loss the same way every step (e.g. by 1/num_microbatches)
+# keeps the forward's gradient from its second step on. The backward writes
+# it in stream order; no host synchronisation is involved.
+_upstream_hint: dict[int, torch.Tensor] = {}
+
+
+def _hint(dev: torch.device) -> torch.Tensor:
+    idx = dev.index if dev.index is not None else torch.cuda.current_device()
+    t = _upstream_hint.get(idx)
+    if t is None:
+        t = torch.ones(1, dtype=torch.float32, device=dev)
+        _upstream_hint[idx] = t
+    return t
 
 
 def _launch(name: str, fn, *args) -> None:
@@ -123,7 +150,8 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return stream
 
 
-def launch_target_check(target: torch.Tensor, vocab_size: int) -> _PendingCheck | None:
+def launch_target_check(target: torch.Tensor, vocab_size: int,
+                        on_side_stream: bool = True) -> _PendingCheck | None:
     """Start the target check of cross_entropy.py:79-81 without blocking.
 
     One kernel counts targets outside ``[0, vocab_size)`` and the counts are
@@ -141,6 +169,18 @@ def launch_target_check(target: torch.Tensor, vocab_size: int) -> _PendingCheck 
         return None
     slots = lib.nmce_validate_slots(n)
     main = torch.cuda.current_stream(t.device)
+    if not on_side_stream:
+        # On the loss stream, ahead of a kernel that fills every compute unit
+        # for its whole run (the one-pass forward), so that the host's wait
+        # ends early instead of after that kernel.
+        counts = torch.empty(slots, dtype=torch.int32, device=t.device)
+        _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
+                vocab_size, counts.data_ptr(), main.cuda_stream)
+        host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
+        host.copy_(counts, non_blocking=True)
+        event = torch.cuda.Event()
+        event.record(main)
+        return _PendingCheck(host, event)
     side = _side_stream(t.device)
     side.wait_stream(main)  # the targets are complete in the current stream's order
     with torch.cuda.stream(side):
@@ -238,6 +278,68 @@ def _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, 
     return loss
 
 
+def _one_pass_rows(logits: torch.Tensor, world_size: int, inplace) -> torch.Tensor | None:
+    """``[rows, V]`` view of ``logits`` when the one-pass kernel takes them:
+    TP = 1, no in-place gradient asked for, V a whole number of 16-byte vectors
+    within the kernel's limit, rows 16-byte aligned. Otherwise None."""
+    if world_size != 1 or inplace or logits.dtype not in (torch.float32, torch.bfloat16):
+        return None
+    rows = _as_rows(logits)
+    if rows is None or rows.shape[0] == 0:
+        return None
+    es = rows.element_size()
+    V = rows.shape[1]
+    ld = rows.stride(0) if rows.shape[0] > 1 else V
+    if (V * es) % 16 or (ld * es) % 16 or rows.data_ptr() % 16:
+        return None
+    if V > _lib.load().nmce_ce_fwd_bwd_max_vocab(_lib.dtype_code(rows.dtype)):
+        return None
+    return rows
+
+
+def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end):
+    """Forward of the whole vocabulary that also writes the gradient of the mean
+    for the upstream value in ``_hint`` into a new buffer, from the same single
+    read of the logits (nmce_ce_fwd_bwd). Returns the flat per-token loss; the
+    backward keeps that gradient unless its upstream value differs."""
+    _check_inputs(logits, target, vocab_start, vocab_end)
+    lib = _lib.load()
+    dev = logits.device
+    n, V = rows.shape
+    ld = rows.stride(0) if n > 1 else V
+    tgt = target.reshape(-1)
+    if not tgt.is_contiguous():
+        tgt = tgt.contiguous()
+    out = torch.empty((3, n), dtype=torch.float32, device=dev)  # loss, max, exp-sum - 1
+    loss, row_stat = out[0], out[1:]
+    grad = torch.empty((n, V), dtype=rows.dtype, device=dev)
+    assumed = torch.empty(1, dtype=torch.float32, device=dev)
+    _launch("nmce_ce_fwd_bwd", lib.nmce_ce_fwd_bwd, rows.data_ptr(), grad.data_ptr(),
+            _lib.dtype_code(rows.dtype), n, V, ld, V, tgt.data_ptr(), loss.data_ptr(),
+            row_stat[0].data_ptr(), row_stat[1].data_ptr(), _hint(dev).data_ptr(),
+            assumed.data_ptr(), float(n), _lib.stream_handle(dev))
+    ctx.vocab_start = vocab_start
+    ctx.logits_shape = logits.shape
+    ctx.ld = ld
+    ctx.save_for_backward(rows, tgt, row_stat, grad, assumed)
+    return loss
+
+
+def _ce_backward_one_pass(ctx, go, gdiv):
+    """Backward after ``_ce_forward_one_pass``: the kernel leaves the buffer as it
+    is when ``go`` is the assumed upstream value and rewrites it from the
+    logits otherwise, so the result equals the two-pass backward bit for bit."""
+    rows, tgt, row_stat, grad, assumed = ctx.saved_tensors
+    lib = _lib.load()
+    n, V = rows.shape
+    _launch("nmce_ce_bwd_scaled_unless", lib.nmce_ce_bwd_scaled_unless,
+            rows.data_ptr(), grad.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, V,
+            tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
+            go.data_ptr(), gdiv, assumed.data_ptr(), _hint(rows.device).data_ptr(),
+            _lib.stream_handle(rows.device))
+    return grad.view(ctx.logits_shape)
+
+
 def _grad_operand(grad_output):
     """(fp32 tensor, row stride) for the kernels; stride 0 for an expanded
     scalar such as the gradient torch's MeanBackward passes."""
@@ -308,9 +410,15 @@ class _VocabParallelCrossEntropyMean(torch.autograd.Function):
     """
 
     @staticmethod
-    def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None):
-        loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
-                           inplace)
+    def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None,
+                one_pass=True):
+        rows = _one_pass_rows(logits, world_size, inplace) if one_pass else None
+        ctx.one_pass = rows is not None
+        if ctx.one_pass:
+            loss = _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end)
+        else:
+            loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
+                               inplace)
         ctx.n_tokens = loss.numel()
         return loss.mean()
 
@@ -319,8 +427,12 @@ class _VocabParallelCrossEntropyMean(torch.autograd.Function):
         go = grad_output.reshape(1)
         if go.dtype != torch.float32:
             go = go.float()
-        grad = _ce_backward(ctx, go, 0, float(max(ctx.n_tokens, 1)))
-        return grad, None, None, None, None, None, None
+        gdiv = float(max(ctx.n_tokens, 1))
+        if ctx.one_pass:
+            grad = _ce_backward_one_pass(ctx, go, gdiv)
+        else:
+            grad = _ce_backward(ctx, go, 0, gdiv)
+        return grad, None, None, None, None, None, None, None
 
 
 def vocab_parallel_cross_entropy(
@@ -332,6 +444,7 @@ def vocab_parallel_cross_entropy(
     *,
     inplace: bool | None = None,
     validate: bool = True,
+    one_pass: bool = True,
 ) -> torch.Tensor:
     """Mean cross-entropy loss from vocab-sharded ``logits`` (cross_entropy.py:68-85).
 
@@ -339,15 +452,28 @@ def vocab_parallel_cross_entropy(
     global token ids; ``ctx`` provides ``tp_size`` and ``tp_group``. Returns a
     0-dim fp32 tensor. ``validate=False`` skips the host-synchronising target
     check (the kernels never read out of bounds either way).
+
+    At TP = 1, when the rows fit the one-pass kernel (V a whole number of
+    16-byte vectors, at most 65536 bf16 or 32768 fp32 columns, rows 16-byte
+    aligned) and no in-place gradient is asked for, the forward reads the
+    logits once and also writes their gradient, for the upstream value the
+    previous backward received (1.0 at first), into a new buffer; the backward
+    rewrites it from the logits only when its upstream value differs. Results
+    are bit-identical
+    to the two-pass path, which ``one_pass=False`` selects, and which
+    ``inplace=True`` selects to write the gradient into the logits' storage
+    instead of a new buffer.
     """
     _check_inputs(logits, target, vocab_start, vocab_end)
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
-    pending = launch_target_check(target, vocab_size) if validate else None
+    one_pass_rows = one_pass and _one_pass_rows(logits, ctx.tp_size, inplace) is not None
+    pending = (launch_target_check(target, vocab_size, on_side_stream=not one_pass_rows)
+               if validate else None)
     # The loss kernels are enqueued before the host waits for the check, so
     # the GPU is busy while the host reads the counts. They never read out of
     # bounds on a bad target; their result is discarded when the check fails.
     loss = _VocabParallelCrossEntropyMean.apply(
-        logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace)
+        logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, one_pass)
     if pending is not None:
         pending.raise_if_bad()
     return loss

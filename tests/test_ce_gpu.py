@@ -334,7 +334,8 @@ def test_inplace_on_nonleaf_logits_with_lm_head():
     t = torch.randint(0, 1000, (2, 64), generator=g).to(DEV)
     logits = h @ w.t()
     storage = logits.data_ptr()
-    loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, 1000, nmce.ParallelContext.single())
+    loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, 1000, nmce.ParallelContext.single(),
+                                             inplace=True)
     loss.backward()
     assert logits.data_ptr() == storage
     h64 = h.detach().double().requires_grad_(True)
@@ -373,7 +374,7 @@ def test_inplace_bumps_version_counter():
     logits = x * 2.0
     side = (logits * logits).sum()  # saves `logits`
     loss = nmce.vocab_parallel_cross_entropy(logits, torch.zeros(4, dtype=torch.long, device=DEV),
-                                             0, 64, nmce.ParallelContext.single())
+                                             0, 64, nmce.ParallelContext.single(), inplace=True)
     with pytest.raises(RuntimeError, match="modified by an inplace operation"):
         (loss + side).backward()
 
@@ -653,3 +654,95 @@ def test_slab_at_the_flat_kernel_limit():
     assert_bf16_close(grad[rows].double().cpu().numpy(), og, what="grad", atol=1e-30)
     del x, grad
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(3, 37, 1000), (2, 512, 32000), (1, 64, 50304), (4, 8, 8)])
+def test_one_pass_is_bit_identical(dtype, shape):
+    """The wrapper's one-pass path (TP = 1) against its two-pass path on the same
+    values: the loss, and the gradient for the upstream value the forward
+    assumed (``loss.backward()``, the buffer kept as written) and for others
+    (0.5, 0.37 and 3.0: rewritten from the logits), all bit for bit. Widths of
+    1 to 8 vectors per lane and a vocabulary of one vector per row; the logits
+    are left as they were."""
+    import nmce
+    b, s, v = shape
+    if v > nmce._lib.load().nmce_ce_fwd_bwd_max_vocab(nmce._lib.dtype_code(dtype)):
+        pytest.skip("wider than the one-pass kernel")
+    print(f"[gpu] one-pass {dtype} {shape}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    base = (torch.randn(b, s, v, device=DEV, generator=g) * 3.0).to(dtype)
+    t = torch.randint(0, v, (b, s), device=DEV, generator=g)
+    ctx = nmce.ParallelContext.single()
+    for upstream in (1.0, 0.5, 0.37, 3.0):
+        out = []
+        for one_pass in (True, False):
+            leaf = base.detach().clone().requires_grad_(True)
+            logits = leaf * 1.0
+            before = logits.detach().clone()
+            loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, inplace=False,
+                                                     one_pass=one_pass)
+            (loss * upstream).backward()
+            assert torch.equal(logits.detach(), before), "the logits were modified"
+            out.append((loss.detach(), leaf.grad.detach()))
+        (l1, g1), (l2, g2) = out
+        assert torch.equal(l1, l2), (upstream, l1.item(), l2.item())
+        if dtype == torch.bfloat16:
+            g1, g2 = g1.view(torch.int16), g2.view(torch.int16)
+        assert torch.equal(g1, g2), f"gradient differs at upstream {upstream}"
+
+
+def test_one_pass_falls_back():
+    """Rows the one-pass kernel does not take run the two-pass path with the
+    same results: a width that is not a whole number of vectors, a width past
+    the kernel's limit, a row stride off the 16-byte grid, TP = 1 with
+    ``inplace=True`` (which writes into the logits' storage)."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(12)
+    cases = [torch.randn(4, 1001, device=DEV, generator=g),
+             torch.randn(2, 70000, device=DEV, generator=g).to(torch.bfloat16),
+             torch.randn(4, 1030, device=DEV, generator=g)[:, :1024]]
+    for x in cases:
+        t = torch.randint(0, x.shape[1], (x.shape[0],), device=DEV, generator=g)
+        grads = []
+        for one_pass in (True, False):
+            leaf = x.detach().clone().requires_grad_(True)
+            nmce.vocab_parallel_cross_entropy(leaf * 1.0, t, 0, x.shape[1], ctx, inplace=False,
+                                              one_pass=one_pass).backward()
+            grads.append(leaf.grad)
+        assert torch.equal(grads[0], grads[1])
+    x = torch.randn(4, 1024, device=DEV, generator=g)
+    t = torch.randint(0, 1024, (4,), device=DEV, generator=g)
+    logits = x.clone().requires_grad_(True) * 1.0
+    storage = logits.data_ptr()
+    nmce.vocab_parallel_cross_entropy(logits, t, 0, 1024, ctx, inplace=True).backward()
+    assert logits.data_ptr() == storage
+    assert torch.allclose(logits.detach().double().sum(-1), torch.zeros(4, device=DEV,
+                          dtype=torch.float64), atol=1e-6)  # the storage holds the gradient
+
+
+def test_one_pass_follows_the_upstream_value():
+    """The one-pass forward computes the gradient for the upstream value the
+    last backward received: a loss scaled by 0.25 every step has its first
+    backward rewrite the gradient and records 0.25, after which the forward's
+    gradient stands. Both steps are bit-identical to the two-pass path."""
+    import nmce
+    from nmce import cross_entropy as ce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(13)
+    x = torch.randn(64, 4096, device=DEV, generator=g).to(torch.bfloat16)
+    t = torch.randint(0, 4096, (64,), device=DEV, generator=g)
+    hint = ce._hint(torch.device(DEV))
+    hint.fill_(1.0)
+    for step in range(2):
+        grads = []
+        for one_pass in (True, False):
+            leaf = x.clone().requires_grad_(True)
+            loss = nmce.vocab_parallel_cross_entropy(leaf * 1.0, t, 0, 4096, ctx,
+                                                     one_pass=one_pass)
+            (loss * 0.25).backward()
+            grads.append(leaf.grad.view(torch.int16))
+        assert torch.equal(grads[0], grads[1]), f"step {step}"
+        assert hint.item() == 0.25
+    hint.fill_(1.0)
