@@ -7,7 +7,10 @@ its host wait cannot be captured) and replay it on new data copied into the
 static inputs. Each replay must give exactly the eager result on the same
 data (the kernels are deterministic), with eager work and synchronisations
 between the replays. The fused LM head + loss is captured the same way; its
-backward's library GEMMs run inside the graph too.
+backward's library GEMMs run inside the graph too. The one-pass path is
+captured with a scaled loss as well: the upstream value its forward assumes
+comes from a device tensor that the backward writes, so replays keep the
+forward's gradient.
 """
 
 from __future__ import annotations
@@ -123,3 +126,42 @@ def test_fused_step_replays_exactly():
         assert got[0] == le.item(), f"replay {rep}: loss {got[0]} vs eager {le.item()}"
         assert torch.equal(got[1], xe.grad), f"replay {rep}: hidden gradient differs"
         assert torch.equal(got[2], we.grad), f"replay {rep}: weight gradient differs"
+
+
+def test_one_pass_scaled_loss_replays_exactly():
+    """The one-pass path inside a graph with the loss scaled by 0.5 each step (as
+    a pipeline scales by 1/num_microbatches): the upstream value the forward
+    assumes comes from a device tensor the backward writes, so replays keep
+    the forward's gradient and match eager steps bit for bit."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    n, v = 512, 8192
+    logits = torch.zeros(n, v, dtype=torch.bfloat16, device=DEV, requires_grad=True)
+    target = torch.zeros(n, dtype=torch.int64, device=DEV)
+
+    def step():
+        logits.grad = None
+        loss = nmce.vocab_parallel_cross_entropy(logits, target, 0, v, ctx, validate=False)
+        (loss * 0.5).backward()
+        return loss.detach()
+
+    graph, static_loss = _capture(step)
+    g = torch.Generator().manual_seed(8)
+    for rep in range(3):
+        x = (torch.randn(n, v, generator=g) * 2.0).to(torch.bfloat16)
+        t = torch.randint(0, v, (n,), generator=g)
+        with torch.no_grad():
+            logits.copy_(x.to(DEV))
+        target.copy_(t.to(DEV))
+        graph.replay()
+        torch.cuda.synchronize()
+        got = (static_loss.item(), logits.grad.clone())
+        xe = x.to(DEV).requires_grad_(True)
+        le = nmce.vocab_parallel_cross_entropy(xe, t.to(DEV), 0, v, ctx, one_pass=False)
+        (le * 0.5).backward()
+        torch.cuda.synchronize()
+        assert got[0] == le.item(), f"replay {rep}: loss {got[0]} vs eager {le.item()}"
+        assert torch.equal(got[1].view(torch.int16), xe.grad.view(torch.int16)), \
+            f"replay {rep}: gradient differs from the two-pass eager step"
+    from nmce import cross_entropy as ce
+    ce._hint(torch.device(DEV)).fill_(1.0)
