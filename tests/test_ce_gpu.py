@@ -746,3 +746,37 @@ def test_one_pass_follows_the_upstream_value():
         assert torch.equal(grads[0], grads[1]), f"step {step}"
         assert hint.item() == 0.25
     hint.fill_(1.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_one_pass_extreme_rows(dtype):
+    """The one-pass path against the two-pass path, bit for bit, on rows at the
+    edges: -inf entries (30% of each row, never the target), maxima tied
+    across half a row, targets leading by 40 and 80, logits of scale 60."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator().manual_seed(14)
+    n, v = 256, 4096
+    x = torch.randn(n, v, generator=g) * 2.0
+    t = torch.randint(0, v, (n,), generator=g)
+    mask = torch.rand(n, v, generator=g) < 0.3
+    mask[torch.arange(n), t] = False
+    x[:64][mask[:64]] = float("-inf")
+    x[64:128, : v // 2] = x[64:128].max()
+    x[128:160][torch.arange(32), t[128:160]] += 40.0
+    x[160:192][torch.arange(32), t[160:192]] += 80.0
+    x[192:] *= 30.0
+    x, t = x.to(dtype).to(DEV), t.to(DEV)
+    for upstream in (1.0, 0.7):
+        out = []
+        for one_pass in (True, False):
+            leaf = x.clone().requires_grad_(True)
+            loss = nmce.vocab_parallel_cross_entropy(leaf * 1.0, t, 0, v, ctx, inplace=False,
+                                                     one_pass=one_pass)
+            (loss * upstream).backward()
+            out.append((loss.detach(), leaf.grad))
+        assert torch.equal(out[0][0], out[1][0]) or (out[0][0].isnan() and out[1][0].isnan())
+        a, b = out[0][1], out[1][1]
+        if dtype == torch.bfloat16:
+            a, b = a.view(torch.int16), b.view(torch.int16)
+        assert torch.equal(a, b), f"gradient differs at upstream {upstream}"
