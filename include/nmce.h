@@ -175,14 +175,17 @@ int nmce_ce_bwd_scaled_unless(const void* logits, void* grad, int dtype, int64_t
  * One-pass forward and backward at TP = 1 (cross_entropy.py:17-65 with the
  * mean of :85, world_size == 1). Each row is read once and held on chip; the
  * kernel writes g_max, g_sumexp_m1 and loss, and the gradient for the
- * upstream value grad_expected[0] of the mean (grad_expected[0] / gout_div per
- * token) into `grad`, a separate buffer (the row's target logit is read back
- * from the logits); the value used goes to grad_assumed[0]. Both are device
- * pointers to one float. Every output is bit-identical to nmce_ce_fwd
- * followed by nmce_ce_bwd_scaled with grad_output = {grad_expected[0]} and
- * gout_stride = 0. The backward is then nmce_ce_bwd_scaled_unless(...,
- * assumed = grad_assumed, ...), which rewrites `grad` from the logits only
- * when the real upstream value differs.
+ * upstream value u of the mean (u / gout_div per token) into `grad`, where
+ * u = grad_expected[0], or 1.0 when that is zero, subnormal, infinite or NaN;
+ * u goes to grad_assumed[0]. Both are device pointers to one float. `grad`
+ * is either a separate buffer or the logits themselves (grad == logits,
+ * ld_grad == ld): the row's target logit is read before the row is
+ * overwritten. Every output is bit-identical to nmce_ce_fwd followed by
+ * nmce_ce_bwd_scaled with grad_output = {u} and gout_stride = 0.
+ * The backward is then, for a separate buffer,
+ * nmce_ce_bwd_scaled_unless(..., assumed = grad_assumed, ...), which
+ * rewrites `grad` from the logits only when the real upstream value differs;
+ * in place, nmce_ce_grad_rescale_unless.
  * Requirements: vocab a whole number of 16-byte vectors and at most
  * nmce_ce_fwd_bwd_max_vocab(dtype) (65536 bf16, 32768 fp32); logits, grad
  * and both row strides 16-byte aligned. No counterpart call in the reference,
@@ -193,6 +196,22 @@ int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, i
                     int64_t ld, int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
                     float* g_sumexp_m1, const float* grad_expected, float* grad_assumed,
                     float gout_div, void* stream);
+
+/*
+ * Backward after an in-place nmce_ce_fwd_bwd (grad == logits), whose
+ * gradient was written for the upstream value assumed[0]: when
+ * grad_output[0] equals it, every workgroup returns at once; otherwise every
+ * entry of `grad` is multiplied by grad_output[0] / assumed[0] in fp32 and
+ * rounded back to the gradient's dtype (cross_entropy.py:64: the gradient is
+ * linear in grad_output). The logits are gone, so this cannot recompute; the
+ * result is within two units in the last place of the gradient dtype of the
+ * recomputed one, and equal to it when the ratio is a power of two.
+ * grad_output[0] also goes to `observed` (may be NULL), the next forward's
+ * grad_expected. Same layout requirements as nmce_ce_fwd_bwd.
+ */
+int nmce_ce_grad_rescale_unless(void* grad, int dtype, int64_t n_rows, int64_t vocab,
+                                int64_t ld_grad, const float* grad_output, const float* assumed,
+                                float* observed, void* stream);
 
 /*
  * Measurement support (no counterpart in the reference): a plain copy of

@@ -270,6 +270,18 @@ __device__ __forceinline__ void set_target(float* y, const T* px, int64_t d, flo
   }
 }
 
+// set_target with the target's logit xt already known (the one-pass kernel
+// broadcasts it before the row is overwritten).
+template <int K>
+__device__ __forceinline__ void set_target_value(float* y, float xt, int64_t d, float M,
+                                                 float T1, float g) {
+  if (static_cast<uint64_t>(d) < static_cast<uint64_t>(K)) {
+    const float yt = target_grad(xt, M, T1, g);
+#pragma unroll
+    for (int k = 0; k < K; ++k) y[k] = (k == d) ? yt : y[k];
+  }
+}
+
 template <typename T, bool kVec, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
 __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
@@ -395,17 +407,28 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
   }
 }
 
+// The upstream value a one-pass forward computes the gradient for: the hint,
+// or 1.0 (loss.backward()'s value) when the hint is zero, subnormal, infinite
+// or NaN. A gradient written for such a value could not be rescaled to the
+// real one, which the in-place form relies on after a miss.
+__device__ __forceinline__ float usable_hint(float h) {
+  const float a = fabsf(h);
+  return (a >= FLT_MIN && a <= FLT_MAX) ? h : 1.0f;
+}
+
 // Forward and backward of whole-vocabulary rows (TP = 1) in one read of the
 // logits. Each workgroup walks rows blockIdx.x, + gridDim.x, ... and holds a
 // row in registers (at most kVec vectors per lane; rows 16-byte aligned, V a
 // whole number of vectors). It folds the row into (max, sum - 1) in
 // ce_stats_kernel's order and merges exactly as that kernel does, issues the
 // loads of its next row, writes the loss and the statistics, then writes the
-// gradient for the upstream value expect[0] of the mean (expect[0] / gdiv
-// per token) with ce_bwd_flat_kernel's arithmetic, from the registers; the
-// value used goes to assumed[0]. Every output is bit-identical to nmce_ce_fwd
-// followed by nmce_ce_bwd_scaled with that upstream value; the backward runs
-// only when the real value differs.
+// gradient for the upstream value usable_hint(expect[0]) of the mean (that
+// value / gdiv per token) with ce_bwd_flat_kernel's arithmetic, from the
+// registers; the value used goes to assumed[0]. The target's logit is read
+// once, before any lane writes, and shared through LDS, so g may be x itself
+// (ldg == ld): the row is then overwritten by its gradient. Every output is
+// bit-identical to nmce_ce_fwd followed by nmce_ce_bwd_scaled with that
+// upstream value; the backward runs only when the real value differs.
 template <typename T, int kVec, int kBlock = kStatsBlock>
 __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
@@ -417,11 +440,11 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
   constexpr int kWaves = kBlock / 64;
   constexpr bool kExact = sizeof(T) == 4;
   static_assert(kVec % 2 == 0, "vectors are folded in pairs");
-  const float expect = expect_in[0];
+  const float expect = usable_hint(expect_in[0]);
   if (blockIdx.x == 0 && threadIdx.x == 0) assumed[0] = expect;
   __shared__ float sm_m[kWaves];
   __shared__ float sm_s[kWaves];
-  __shared__ float sm_row[2];
+  __shared__ float sm_row[3];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -485,11 +508,13 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
         loss[row] = log1pf(T1) - (xt - M);
         sm_row[0] = M;
         sm_row[1] = T1;
+        sm_row[2] = xt;
       }
     }
     __syncthreads();
     const float M = sm_row[0];
     const float T1 = sm_row[1];
+    const float xt = sm_row[2];
     const float scale = go / (1.0f + T1);
     const int64_t lt = target[row];
     T* gr = g + row * ldg;
@@ -501,13 +526,53 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
         E::unpack(cur[k], f);
 #pragma unroll
         for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
-        set_target<EPV>(y, xr + i * EPV, lt - i * EPV, M, T1, go);
+        set_target_value<EPV>(y, xt, lt - i * EPV, M, T1, go);
         store_stream(reinterpret_cast<u32x4*>(gr) + i, E::pack(y));
       }
     }
 #pragma unroll
     for (int k = 0; k < kVec; ++k) cur[k] = nxt[k];
     __syncthreads();  // sm_row is rewritten for the next row
+  }
+}
+
+// The backward of an in-place one-pass forward (ce_fwdbwd_kernel with g == x,
+// the logits already overwritten): when the real upstream value gout[0]
+// differs from the assumed[0] the gradient was written for, every entry is
+// scaled by gout[0] / assumed[0] (each is linear in the upstream value:
+// cross_entropy.py:64). Rows as in the one-pass kernel (16-byte aligned, V a
+// whole number of vectors), walked on its grid, so that a hit costs one short
+// launch. gout[0] also goes to observed[0] for the next forward.
+template <typename T, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
+__global__ __launch_bounds__(kBlock) void ce_grad_rescale_kernel(
+    T* g, int64_t n_rows, int64_t V, int64_t ldg, const float* __restrict__ gout,
+    const float* __restrict__ assumed, float* __restrict__ observed) {
+  using E = Elem<T>;
+  constexpr int EPV = E::kPerVec;
+  const float gv = gout[0];
+  if (observed && blockIdx.x == 0 && threadIdx.x == 0) observed[0] = gv;
+  const float a = assumed[0];
+  if (gv == a) return;
+  const float ratio = gv / a;
+  const int64_t nvec = V / EPV;
+  for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x) {
+    u32x4* gr = reinterpret_cast<u32x4*>(g + row * ldg);
+    for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += kUnroll * kBlock) {
+      u32x4 v[kUnroll];
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u)
+        if (i0 + u * kBlock < nvec) v[u] = load_stream(gr + i0 + u * kBlock);
+#pragma unroll
+      for (int u = 0; u < kUnroll; ++u) {
+        if (i0 + u * kBlock < nvec) {
+          float f[EPV];
+          E::unpack(v[u], f);
+#pragma unroll
+          for (int k = 0; k < EPV; ++k) f[k] *= ratio;
+          store_stream(gr + i0 + u * kBlock, E::pack(f));
+        }
+      }
+    }
   }
 }
 
@@ -788,7 +853,7 @@ int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, i
   if (!logits || !grad || !target || !loss || !g_max || !g_sumexp_m1 || !grad_expected ||
       !grad_assumed)
     return NMCE_EINVAL_PTR;
-  if (grad == logits) return NMCE_EINVAL_PTR;  // the target's logit is read back from the row
+  if (grad == logits && ld_grad != ld) return NMCE_EINVAL_SHAPE;
   if (reinterpret_cast<uintptr_t>(logits) % 16 || reinterpret_cast<uintptr_t>(grad) % 16 ||
       (ld * es) % 16 || (ld_grad * es) % 16)
     return NMCE_EINVAL_ALIGN;
@@ -813,6 +878,28 @@ int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, i
                                                loss, g_max, g_sumexp_m1, grad_expected,
                                                grad_assumed, gout_div, st);
   }
+  return launch_status();
+}
+
+int nmce_ce_grad_rescale_unless(void* grad, int dtype, int64_t n_rows, int64_t vocab,
+                                int64_t ld_grad, const float* grad_output, const float* assumed,
+                                float* observed, void* stream) {
+  if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
+  const int64_t es = dtype == NMCE_F32 ? 4 : 2;
+  if (n_rows < 0 || vocab < 1 || ld_grad < vocab || vocab % (16 / es)) return NMCE_EINVAL_SHAPE;
+  if (n_rows == 0) return NMCE_OK;
+  if (!grad || !grad_output || !assumed) return NMCE_EINVAL_PTR;
+  if (reinterpret_cast<uintptr_t>(grad) % 16 || (ld_grad * es) % 16) return NMCE_EINVAL_ALIGN;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const dim3 grid(one_pass_grid(n_rows)), block(kBwdBlock);
+  if (dtype == NMCE_F32)
+    hipLaunchKernelGGL(ce_grad_rescale_kernel<float>, grid, block, 0, st,
+                       static_cast<float*>(grad), n_rows, vocab, ld_grad, grad_output, assumed,
+                       observed);
+  else
+    hipLaunchKernelGGL(ce_grad_rescale_kernel<uint16_t>, grid, block, 0, st,
+                       static_cast<uint16_t*>(grad), n_rows, vocab, ld_grad, grad_output, assumed,
+                       observed);
   return launch_status();
 }
 

@@ -44,6 +44,7 @@ SIGNATURES: dict[str, tuple] = {
     "nmce_ce_fwd_bwd_max_vocab": (_i64, [_c_int]),
     "nmce_ce_fwd_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p,
                                  ctypes.c_float, _p]),
+    "nmce_ce_grad_rescale_unless": (_c_int, [_p, _c_int, _i64, _i64, _i64, _p, _p, _p, _p]),
     "nmce_lmhead_ce_fwd_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "nmce_lmhead_ce_fwd_stats": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p,
                                           _p, _i64, _p]),

@@ -17,23 +17,28 @@ Differences from the reference, all deliberate:
   (exactly 1), so a confident token's loss log1p(sum - 1) and target gradient
   -(sum - 1)/sum * g keep their relative precision; the reference's log(sum)
   and softmax - 1 give the same values up to fp32 cancellation near 1.
-* The wrapper at TP = 1, on rows that fit (V a whole number of 16-byte
+* The wrapper at TP = 1, when a gradient is wanted (grad mode on and the
+  logits require grad) and the rows fit (V a whole number of 16-byte
   vectors, at most 65536 bf16 / 32768 fp32 columns), reads the logits once:
   its forward also writes the gradient for the upstream value that the last
-  backward received (1.0, as for ``loss.backward()``, before the first) into
-  a new ``[tokens, vocab]`` buffer -- as the reference's forward computes the
-  softmax its backward returns -- and the backward rewrites it from the
-  logits only when its upstream value differs. A loss scaled the same way
-  every step keeps the forward's gradient from the second step on. Always
-  bit-identical to the two-pass path; ``one_pass=False`` turns it off.
-* Otherwise (TP > 1, other rows, the per-token Function, or ``inplace=True``)
-  the gradient is written **in place** into the logits storage when the
+  backward from the same call site received (1.0, as for
+  ``loss.backward()``, before the first) -- as the reference's forward
+  computes the softmax its backward returns (:48-49). A loss scaled the same
+  way every step keeps the forward's gradient from the second step on. The
+  gradient goes into the logits' storage when the gradient is written in
+  place (below), else into a new ``[tokens, vocab]`` buffer. A backward whose
+  upstream value differs rewrites a separate buffer from the logits
+  (bit-identical to the two-pass path), and rescales an in-place one (within
+  two units in the last place; exact for a power-of-two ratio).
+  ``one_pass=False`` turns it off.
+* The gradient is written **in place** into the logits storage when the
   logits are a non-leaf tensor (as at model.py:277-281, where they come
-  straight from the LM-head matmul, which does not save them). Pass
-  ``inplace=False`` to keep the logits intact; leaf tensors are never
-  overwritten. The version counter of the logits is bumped after an in-place
-  write, so any other autograd node that saved them fails loudly instead of
-  reading gradients.
+  straight from the LM-head matmul, which does not save them): by the
+  backward on the two-pass path, and already by the forward on the one-pass
+  path. Pass ``inplace=False`` to keep the logits intact; leaf tensors are
+  never overwritten. The version counter of the logits is bumped after an
+  in-place write, so any other autograd node that saved them fails loudly
+  instead of reading gradients.
 * With ``tp_size > 1`` the three dependent all-reduces (:23, :38, :43) become
   one all-gather of packed ``[3, tokens]`` statistics followed by a local
   combine.
@@ -48,6 +53,8 @@ must be built; anything else raises.
 
 from __future__ import annotations
 
+import sys
+
 import torch
 import torch.distributed as dist
 
@@ -58,22 +65,31 @@ from . import _lib
 # stream, so a caller can time each kernel inside a running workload.
 kernel_timeline: list | None = None
 
-# Per device, one float: the upstream value of the mean that the last
-# one-pass backward received (the 1.0 of ``loss.backward()`` until one has
-# run). The one-pass forward computes the gradient for it, so a training loop
-# that scales its loss the same way every step (e.g. by 1/num_microbatches)
-# keeps the forward's gradient from its second step on. The backward writes
-# it in stream order; no host synchronisation is involved.
-_upstream_hint: dict[int, torch.Tensor] = {}
+# Per (device, call site): one float, the upstream value of the mean that the
+# last one-pass backward of a loss computed at that site received (the 1.0 of
+# ``loss.backward()`` until one has run). The one-pass forward computes the
+# gradient for it, so a training loop that scales its loss the same way every
+# step (e.g. by 1/num_microbatches, pipeline.py:127) keeps the forward's
+# gradient from its second step on, and two losses scaled differently at two
+# sites do not spoil each other's guess. The backward writes it in stream
+# order; no host synchronisation is involved.
+_upstream_hints: dict[tuple, torch.Tensor] = {}
 
 
-def _hint(dev: torch.device) -> torch.Tensor:
+def _site_hint(dev: torch.device, site: tuple) -> torch.Tensor:
     idx = dev.index if dev.index is not None else torch.cuda.current_device()
-    t = _upstream_hint.get(idx)
+    key = (idx,) + site
+    t = _upstream_hints.get(key)
     if t is None:
         t = torch.ones(1, dtype=torch.float32, device=dev)
-        _upstream_hint[idx] = t
+        _upstream_hints[key] = t
     return t
+
+
+def _check_hint(hint: torch.Tensor, dev: torch.device) -> None:
+    if hint.device != dev or hint.dtype != torch.float32 or hint.numel() != 1:
+        raise ValueError("nmce: upstream_hint must be a one-element float32 tensor on the "
+                         "logits' device")
 
 
 def _launch(name: str, fn, *args) -> None:
@@ -226,6 +242,17 @@ def _exchange_stats(local: torch.Tensor, group, world_size: int) -> torch.Tensor
     return gathered.to(local.device) if host else gathered
 
 
+def _resolve_inplace(logits: torch.Tensor, inplace) -> bool:
+    """``inplace=None``: in place iff the logits are a non-leaf tensor. A leaf
+    that requires grad is never overwritten."""
+    if inplace is None:
+        return logits.grad_fn is not None
+    if inplace and logits.grad_fn is None and logits.requires_grad:
+        raise ValueError("nmce: refusing to write the gradient into a leaf tensor; "
+                         "pass inplace=False or None")
+    return bool(inplace)
+
+
 def _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace):
     """Forward of one shard (cross_entropy.py:17-50): returns the flat per-token
     fp32 loss and leaves on ``ctx`` what the backward needs."""
@@ -236,11 +263,7 @@ def _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, 
     V = logits.shape[-1]
 
     rows = _as_rows(logits)
-    if inplace is None:
-        inplace = logits.grad_fn is not None
-    elif inplace and logits.grad_fn is None and logits.requires_grad:
-        raise ValueError("nmce: refusing to write the gradient into a leaf tensor; "
-                         "pass inplace=False or None")
+    inplace = _resolve_inplace(logits, inplace)
     if rows is None:  # not viewable as [rows, V]: work on a contiguous copy
         rows = logits.contiguous().view(-1, V)
         inplace = False
@@ -278,11 +301,11 @@ def _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, 
     return loss
 
 
-def _one_pass_rows(logits: torch.Tensor, world_size: int, inplace) -> torch.Tensor | None:
+def _one_pass_rows(logits: torch.Tensor, world_size: int) -> torch.Tensor | None:
     """``[rows, V]`` view of ``logits`` when the one-pass kernel takes them:
-    TP = 1, no in-place gradient asked for, V a whole number of 16-byte vectors
-    within the kernel's limit, rows 16-byte aligned. Otherwise None."""
-    if world_size != 1 or inplace or logits.dtype not in (torch.float32, torch.bfloat16):
+    TP = 1, V a whole number of 16-byte vectors within the kernel's limit,
+    rows 16-byte aligned. Otherwise None."""
+    if world_size != 1 or logits.dtype not in (torch.float32, torch.bfloat16):
         return None
     rows = _as_rows(logits)
     if rows is None or rows.shape[0] == 0:
@@ -297,11 +320,12 @@ def _one_pass_rows(logits: torch.Tensor, world_size: int, inplace) -> torch.Tens
     return rows
 
 
-def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end):
+def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint, inplace):
     """Forward of the whole vocabulary that also writes the gradient of the mean
-    for the upstream value in ``_hint`` into a new buffer, from the same single
-    read of the logits (nmce_ce_fwd_bwd). Returns the flat per-token loss; the
-    backward keeps that gradient unless its upstream value differs."""
+    for the upstream value in ``hint`` (nmce_ce_fwd_bwd), from the same single
+    read of the logits: into the logits' own storage when ``inplace``, else
+    into a new buffer. Returns the flat per-token loss; the backward keeps that
+    gradient unless its upstream value differs."""
     _check_inputs(logits, target, vocab_start, vocab_end)
     lib = _lib.load()
     dev = logits.device
@@ -312,31 +336,72 @@ def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end):
         tgt = tgt.contiguous()
     out = torch.empty((3, n), dtype=torch.float32, device=dev)  # loss, max, exp-sum - 1
     loss, row_stat = out[0], out[1:]
-    grad = torch.empty((n, V), dtype=rows.dtype, device=dev)
+    if inplace:
+        grad, ldg = rows, ld
+    else:
+        grad, ldg = torch.empty((n, V), dtype=rows.dtype, device=dev), V
     assumed = torch.empty(1, dtype=torch.float32, device=dev)
     _launch("nmce_ce_fwd_bwd", lib.nmce_ce_fwd_bwd, rows.data_ptr(), grad.data_ptr(),
-            _lib.dtype_code(rows.dtype), n, V, ld, V, tgt.data_ptr(), loss.data_ptr(),
-            row_stat[0].data_ptr(), row_stat[1].data_ptr(), _hint(dev).data_ptr(),
+            _lib.dtype_code(rows.dtype), n, V, ld, ldg, tgt.data_ptr(), loss.data_ptr(),
+            row_stat[0].data_ptr(), row_stat[1].data_ptr(), hint.data_ptr(),
             assumed.data_ptr(), float(n), _lib.stream_handle(dev))
     ctx.vocab_start = vocab_start
     ctx.logits_shape = logits.shape
     ctx.ld = ld
-    ctx.save_for_backward(rows, tgt, row_stat, grad, assumed)
+    ctx.inplace = inplace
+    ctx.hint = hint
+    ctx.handed_out = False
+    if inplace:
+        # The logits now hold the gradient: make autograd nodes that saved
+        # them fail their version check rather than read it.
+        torch.autograd.graph.increment_version(logits)
+        ctx.grad_buf = logits.detach()
+        ctx.save_for_backward(tgt, row_stat, assumed)
+    else:
+        ctx.save_for_backward(rows, tgt, row_stat, grad, assumed)
     return loss
 
 
 def _ce_backward_one_pass(ctx, go, gdiv):
-    """Backward after ``_ce_forward_one_pass``: the kernel leaves the buffer as it
-    is when ``go`` is the assumed upstream value and rewrites it from the
-    logits otherwise, so the result equals the two-pass backward bit for bit."""
-    rows, tgt, row_stat, grad, assumed = ctx.saved_tensors
+    """Backward after ``_ce_forward_one_pass``. A separate buffer is left as it
+    is when ``go`` is the assumed upstream value and rewritten from the logits
+    otherwise, so the result equals the two-pass backward bit for bit. An
+    in-place one is rescaled instead (the logits are gone). Either way the
+    buffer is handed out once: a second backward through the same graph
+    (``retain_graph=True``) gets a new buffer from the logits, or raises when
+    they hold the gradient."""
     lib = _lib.load()
+    stream = None
+    if ctx.inplace:
+        if ctx.handed_out:
+            raise RuntimeError(
+                "nmce: a second backward through an in-place one-pass loss needs the logits, "
+                "which now hold the gradient; pass inplace=False to differentiate it twice")
+        tgt, row_stat, assumed = ctx.saved_tensors
+        grad = ctx.grad_buf
+        n, V = tgt.numel(), ctx.logits_shape[-1]
+        stream = _lib.stream_handle(grad.device)
+        _launch("nmce_ce_grad_rescale_unless", lib.nmce_ce_grad_rescale_unless,
+                grad.data_ptr(), _lib.dtype_code(grad.dtype), n, V, ctx.ld, go.data_ptr(),
+                assumed.data_ptr(), ctx.hint.data_ptr(), stream)
+        ctx.handed_out = True
+        ctx.grad_buf = None
+        return grad
+    rows, tgt, row_stat, grad, assumed = ctx.saved_tensors
     n, V = rows.shape
+    stream = _lib.stream_handle(rows.device)
+    if ctx.handed_out:
+        fresh = torch.empty((n, V), dtype=rows.dtype, device=rows.device)
+        _launch("nmce_ce_bwd_scaled", lib.nmce_ce_bwd_scaled,
+                rows.data_ptr(), fresh.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, V,
+                tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
+                go.data_ptr(), 0, gdiv, stream)
+        return fresh.view(ctx.logits_shape)
     _launch("nmce_ce_bwd_scaled_unless", lib.nmce_ce_bwd_scaled_unless,
             rows.data_ptr(), grad.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, V,
             tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
-            go.data_ptr(), gdiv, assumed.data_ptr(), _hint(rows.device).data_ptr(),
-            _lib.stream_handle(rows.device))
+            go.data_ptr(), gdiv, assumed.data_ptr(), ctx.hint.data_ptr(), stream)
+    ctx.handed_out = True
     return grad.view(ctx.logits_shape)
 
 
@@ -411,11 +476,14 @@ class _VocabParallelCrossEntropyMean(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None,
-                one_pass=True):
-        rows = _one_pass_rows(logits, world_size, inplace) if one_pass else None
+                hint=None):
+        # ``hint`` (the one-pass path's upstream value) is given only when a
+        # gradient is wanted; without it the forward writes no gradient.
+        rows = _one_pass_rows(logits, world_size) if hint is not None else None
         ctx.one_pass = rows is not None
         if ctx.one_pass:
-            loss = _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end)
+            loss = _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint,
+                                        _resolve_inplace(logits, inplace))
         else:
             loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
                                inplace)
@@ -445,6 +513,7 @@ def vocab_parallel_cross_entropy(
     inplace: bool | None = None,
     validate: bool = True,
     one_pass: bool = True,
+    upstream_hint: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Mean cross-entropy loss from vocab-sharded ``logits`` (cross_entropy.py:68-85).
 
@@ -453,27 +522,44 @@ def vocab_parallel_cross_entropy(
     0-dim fp32 tensor. ``validate=False`` skips the host-synchronising target
     check (the kernels never read out of bounds either way).
 
-    At TP = 1, when the rows fit the one-pass kernel (V a whole number of
-    16-byte vectors, at most 65536 bf16 or 32768 fp32 columns, rows 16-byte
-    aligned) and no in-place gradient is asked for, the forward reads the
-    logits once and also writes their gradient, for the upstream value the
-    previous backward received (1.0 at first), into a new buffer; the backward
-    rewrites it from the logits only when its upstream value differs. Results
-    are bit-identical
-    to the two-pass path, which ``one_pass=False`` selects, and which
-    ``inplace=True`` selects to write the gradient into the logits' storage
-    instead of a new buffer.
+    ``inplace=None`` writes the gradient into the logits' storage when they are
+    a non-leaf tensor (as the LM head's output is); ``False`` never does.
+
+    At TP = 1, when a gradient is wanted (grad mode on, logits requiring grad)
+    and the rows fit the one-pass kernel (V a whole number of 16-byte vectors,
+    at most 65536 bf16 or 32768 fp32 columns, rows 16-byte aligned), the
+    forward reads the logits once and also writes their gradient, for the
+    upstream value the previous backward of this call site received (1.0 at
+    first): in place (the logits hold the gradient once the forward returns)
+    or into a new buffer. The backward redoes it only when its upstream value
+    differs: bit-identical to the two-pass path, which ``one_pass=False``
+    selects, for a new buffer; rescaled, within two units in the last place,
+    in place. ``upstream_hint`` (a one-element fp32 device tensor) replaces
+    the call site's value: the forward assumes what it holds and the backward
+    stores what it receives there.
+
+    On a target outside the vocabulary the ``ValueError`` is raised after the
+    loss kernels were enqueued; on the in-place one-pass path the logits then
+    already hold a (meaningless) gradient.
     """
     _check_inputs(logits, target, vocab_start, vocab_end)
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
-    one_pass_rows = one_pass and _one_pass_rows(logits, ctx.tp_size, inplace) is not None
-    pending = (launch_target_check(target, vocab_size, on_side_stream=not one_pass_rows)
+    hint = None
+    if (one_pass and torch.is_grad_enabled() and logits.requires_grad
+            and _one_pass_rows(logits, ctx.tp_size) is not None):
+        if upstream_hint is None:
+            caller = sys._getframe(1)
+            hint = _site_hint(logits.device, (caller.f_code.co_filename, caller.f_lineno))
+        else:
+            _check_hint(upstream_hint, logits.device)
+            hint = upstream_hint
+    pending = (launch_target_check(target, vocab_size, on_side_stream=hint is None)
                if validate else None)
     # The loss kernels are enqueued before the host waits for the check, so
     # the GPU is busy while the host reads the counts. They never read out of
     # bounds on a bad target; their result is discarded when the check fails.
     loss = _VocabParallelCrossEntropyMean.apply(
-        logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, one_pass)
+        logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, hint)
     if pending is not None:
         pending.raise_if_bad()
     return loss

@@ -170,16 +170,6 @@ def sharded(x_full: np.ndarray, target: np.ndarray, tp: int, grad_output=None):
     return loss, grads, M, S1
 
 
-def bf16_round(x: np.ndarray) -> np.ndarray:
-    """Round fp32/fp64 values to bf16 (nearest even), returned as fp32."""
-    f = np.asarray(x, dtype=np.float32)
-    u = f.view(np.uint32).astype(np.uint64)
-    nan = np.isnan(f)
-    rounded = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
-    out = rounded.astype(np.uint32).view(np.float32)
-    return np.where(nan, np.float32(np.nan), out)
-
-
 def lmhead_closed_form(hidden: np.ndarray, weight: np.ndarray, target: np.ndarray,
                        grad_output=None):
     """Loss and gradients of ``closed_form(hidden @ weight^T)`` in fp64.

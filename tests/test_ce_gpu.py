@@ -695,8 +695,7 @@ def test_one_pass_is_bit_identical(dtype, shape):
 def test_one_pass_falls_back():
     """Rows the one-pass kernel does not take run the two-pass path with the
     same results: a width that is not a whole number of vectors, a width past
-    the kernel's limit, a row stride off the 16-byte grid, TP = 1 with
-    ``inplace=True`` (which writes into the logits' storage)."""
+    the kernel's limit, a row stride off the 16-byte grid."""
     import nmce
     ctx = nmce.ParallelContext.single()
     g = torch.Generator(device=DEV).manual_seed(12)
@@ -712,40 +711,244 @@ def test_one_pass_falls_back():
                                               one_pass=one_pass).backward()
             grads.append(leaf.grad)
         assert torch.equal(grads[0], grads[1])
-    x = torch.randn(4, 1024, device=DEV, generator=g)
-    t = torch.randint(0, 1024, (4,), device=DEV, generator=g)
-    logits = x.clone().requires_grad_(True) * 1.0
-    storage = logits.data_ptr()
-    nmce.vocab_parallel_cross_entropy(logits, t, 0, 1024, ctx, inplace=True).backward()
-    assert logits.data_ptr() == storage
-    assert torch.allclose(logits.detach().double().sum(-1), torch.zeros(4, device=DEV,
-                          dtype=torch.float64), atol=1e-6)  # the storage holds the gradient
 
 
-def test_one_pass_follows_the_upstream_value():
+class _HitRecorder:
+    """Wraps the one-pass backward and records (assumed, received) upstream
+    values: the forward's gradient stands when they are equal."""
+
+    def __init__(self, monkeypatch):
+        from nmce import cross_entropy as ce
+        self.calls = []
+        original = ce._ce_backward_one_pass
+
+        def wrapped(ctx, go, gdiv):
+            assumed = ctx.saved_tensors[-1]
+            self.calls.append((assumed.item(), go.item()))
+            return original(ctx, go, gdiv)
+
+        monkeypatch.setattr(ce, "_ce_backward_one_pass", wrapped)
+
+
+def test_one_pass_follows_the_upstream_value(monkeypatch):
     """The one-pass forward computes the gradient for the upstream value the
     last backward received: a loss scaled by 0.25 every step has its first
-    backward rewrite the gradient and records 0.25, after which the forward's
+    backward rewrite the gradient and record 0.25, after which the forward's
     gradient stands. Both steps are bit-identical to the two-pass path."""
     import nmce
-    from nmce import cross_entropy as ce
+    rec = _HitRecorder(monkeypatch)
     ctx = nmce.ParallelContext.single()
     g = torch.Generator(device=DEV).manual_seed(13)
     x = torch.randn(64, 4096, device=DEV, generator=g).to(torch.bfloat16)
     t = torch.randint(0, 4096, (64,), device=DEV, generator=g)
-    hint = ce._hint(torch.device(DEV))
-    hint.fill_(1.0)
+    hint = torch.ones(1, dtype=torch.float32, device=DEV)
     for step in range(2):
         grads = []
         for one_pass in (True, False):
             leaf = x.clone().requires_grad_(True)
-            loss = nmce.vocab_parallel_cross_entropy(leaf * 1.0, t, 0, 4096, ctx,
-                                                     one_pass=one_pass)
+            loss = nmce.vocab_parallel_cross_entropy(leaf * 1.0, t, 0, 4096, ctx, inplace=False,
+                                                     one_pass=one_pass, upstream_hint=hint)
             (loss * 0.25).backward()
             grads.append(leaf.grad.view(torch.int16))
         assert torch.equal(grads[0], grads[1]), f"step {step}"
         assert hint.item() == 0.25
-    hint.fill_(1.0)
+    assert rec.calls == [(1.0, 0.25), (0.25, 0.25)]
+
+
+def _two_sites(nmce, ctx, a, b, t, v):
+    """Two losses computed at two call sites (two source lines)."""
+    la = nmce.vocab_parallel_cross_entropy(a, t, 0, v, ctx, inplace=False)
+    lb = nmce.vocab_parallel_cross_entropy(b, t, 0, v, ctx, inplace=False)
+    return la, lb
+
+
+def test_one_pass_hints_are_per_call_site(monkeypatch):
+    """Two losses scaled by 1.0 and 0.1, computed at two call sites and
+    differentiated together every step, each keep their own upstream value:
+    from the second step on both forwards' gradients stand. Gradients match
+    the two-pass path bit for bit on every step."""
+    import nmce
+    rec = _HitRecorder(monkeypatch)
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(21)
+    v = 2048
+    x = torch.randn(2, 128, v, device=DEV, generator=g).to(torch.bfloat16)
+    t = torch.randint(0, v, (128,), device=DEV, generator=g)
+    for step in range(3):
+        a = x[0].clone().requires_grad_(True)
+        b = x[1].clone().requires_grad_(True)
+        la, lb = _two_sites(nmce, ctx, a * 1.0, b * 1.0, t, v)
+        (la * 1.0 + lb * 0.1).backward()
+        for leaf, scale in ((a, 1.0), (b, 0.1)):
+            ref = leaf.detach().clone().requires_grad_(True)
+            (nmce.vocab_parallel_cross_entropy(ref * 1.0, t, 0, v, ctx, one_pass=False)
+             * scale).backward()
+            assert torch.equal(leaf.grad.view(torch.int16), ref.grad.view(torch.int16)), step
+    got = sorted(rec.calls[2:])  # steps 2 and 3: both sites hit
+    assert len(rec.calls) == 6
+    assert all(a == b for a, b in rec.calls[2:]), rec.calls
+    assert sorted(set(c[1] for c in got)) == sorted({1.0, np.float32(0.1).item()})
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("shape", [(3, 37, 1000), (2, 512, 32000), (1, 600, 50304), (4, 8, 8)])
+def test_one_pass_in_place(dtype, shape):
+    """Non-leaf logits at TP = 1 (inplace=None): the one-pass forward writes the
+    gradient into the logits' own storage. Upstream 1.0 (the forward's value)
+    and 0.5 (a power-of-two rescale) are bit-identical to the two-pass path
+    (which writes in place too, in its backward); 0.37 and 3.0 are rescaled
+    and within two units in the last place of the gradient's dtype."""
+    import nmce
+    b, s, v = shape
+    if v > nmce._lib.load().nmce_ce_fwd_bwd_max_vocab(nmce._lib.dtype_code(dtype)):
+        pytest.skip("wider than the one-pass kernel")
+    print(f"[gpu] one-pass in place {dtype} {shape}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(15)
+    base = (torch.randn(b, s, v, device=DEV, generator=g) * 3.0).to(dtype)
+    t = torch.randint(0, v, (b, s), device=DEV, generator=g)
+    ctx = nmce.ParallelContext.single()
+    ulp = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -22
+    for upstream in (1.0, 0.5, 0.37, 3.0):
+        out = []
+        for one_pass in (True, False):
+            hint = torch.ones(1, dtype=torch.float32, device=DEV)
+            anchor = torch.zeros((), device=DEV, requires_grad=True)
+            logits = base.clone() + anchor.to(dtype)  # non-leaf, own storage
+            storage = logits.data_ptr()
+            loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, one_pass=one_pass,
+                                                     upstream_hint=hint)
+            grads = []
+            logits.register_hook(lambda gr: grads.append(gr))
+            (loss * upstream).backward()
+            assert grads[0].data_ptr() == storage, "the gradient is not in the logits' storage"
+            out.append((loss.detach(), grads[0].detach().clone()))
+        (l1, g1), (l2, g2) = out
+        assert torch.equal(l1, l2), (upstream, l1.item(), l2.item())
+        if upstream in (1.0, 0.5):
+            a, c = (g1.view(torch.int16), g2.view(torch.int16)) if dtype == torch.bfloat16 \
+                else (g1, g2)
+            assert torch.equal(a, c), f"gradient differs at upstream {upstream}"
+        else:
+            err = (g1.double() - g2.double()).abs()
+            bound = ulp * g2.double().abs() + 1e-38
+            assert bool((err <= bound).all()), f"upstream {upstream}: {err.max().item():.3e}"
+
+
+def test_one_pass_writes_nothing_without_grad():
+    """No gradient wanted, no gradient written: under torch.no_grad(), and for
+    logits that do not require grad, the forward allocates no [N, V] buffer
+    and leaves non-leaf logits as they were; the loss is the two-pass one."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(16)
+    n, v = 4096, 32768
+    x = torch.randn(n, v, device=DEV, generator=g).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    slab = n * v * 2
+    anchor = torch.zeros((), device=DEV, requires_grad=True)
+    logits = x + anchor.to(torch.bfloat16)  # non-leaf: would be written in place
+    ref = nmce.vocab_parallel_cross_entropy(x.clone().requires_grad_(True), t, 0, v, ctx,
+                                            one_pass=False).item()
+    for mode in ("no_grad", "no_requires_grad"):
+        snapshot = logits if mode == "no_grad" else x.clone()
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        before = torch.cuda.memory_allocated()
+        if mode == "no_grad":
+            with torch.no_grad():
+                loss = nmce.vocab_parallel_cross_entropy(snapshot, t, 0, v, ctx)
+        else:
+            loss = nmce.vocab_parallel_cross_entropy(snapshot, t, 0, v, ctx)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated() - before
+        assert peak < slab // 8, f"{mode}: {peak} bytes allocated"
+        assert loss.item() == ref, mode
+        assert torch.equal(snapshot.view(torch.int16), x.view(torch.int16)), mode
+
+
+def test_one_pass_retain_graph():
+    """A second backward through the same graph: a separate one-pass buffer is
+    handed out once, so the leaf's .grad accumulates the first gradient plus
+    one written anew for the second upstream value (bit-identical to the
+    two-pass path); the in-place form has no logits left and raises."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(17)
+    n, v = 256, 8192
+    x = torch.randn(n, v, device=DEV, generator=g).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    grads = []
+    for one_pass in (True, False):
+        leaf = x.clone().requires_grad_(True)
+        loss = nmce.vocab_parallel_cross_entropy(leaf, t, 0, v, ctx, one_pass=one_pass)
+        loss.backward(retain_graph=True)
+        first = leaf.grad.clone()
+        (loss * 0.5).backward()
+        grads.append((first, leaf.grad))
+    assert torch.equal(grads[0][0].view(torch.int16), grads[1][0].view(torch.int16))
+    assert torch.equal(grads[0][1].view(torch.int16), grads[1][1].view(torch.int16))
+    anchor = torch.zeros((), device=DEV, requires_grad=True)
+    loss = nmce.vocab_parallel_cross_entropy(x.clone() + anchor.to(torch.bfloat16), t, 0, v, ctx)
+    loss.backward(retain_graph=True)
+    with pytest.raises(RuntimeError, match="second backward"):
+        loss.backward()
+
+
+def test_c2_full_size_one_pass():
+    """c2 through the wrapper's default path, the configuration the benchmark
+    times: bf16 [8,2048,50304] ~ N(0,1) at TP = 1 runs ce_fwdbwd_kernel<bf16, 8>
+    over 16384 rows on a grid of two workgroups per compute unit, each walking
+    rows with the next row's loads in flight. In place (non-leaf logits) and
+    into a separate buffer, at upstream 1.0 and 0.5, against the two-pass path
+    bit for bit on the whole slab; the loss against a chunked fp64 reference;
+    sampled gradient rows against the oracle."""
+    import nmce
+    print("[gpu] c2 one-pass bf16 [8,2048,50304]", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    N, V = 8 * 2048, 50304
+    x = torch.randn(N, V, device=DEV, generator=gen).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), device=DEV, generator=gen)
+    ref_loss = _torch_ref_rows(x, t)
+    ctx = nmce.ParallelContext.single()
+    tv = t.view(8, 2048)
+    pick = torch.arange(0, N, 509, device=DEV)
+    xs, ts = x[pick].float().cpu().numpy(), t[pick].cpu().numpy()
+    for upstream in (1.0, 0.5):
+        # the two-pass reference, into a separate buffer
+        leaf = x.view(8, 2048, V).clone().requires_grad_(True)
+        loss2 = nmce.vocab_parallel_cross_entropy(leaf, tv, 0, V, ctx, one_pass=False)
+        (loss2 * upstream).backward()
+        ref_grad = leaf.grad.view(N, V)
+        del leaf
+        for inplace in (False, None):
+            hint = torch.ones(1, dtype=torch.float32, device=DEV)
+            anchor = torch.zeros((), device=DEV, requires_grad=True)
+            logits = x.view(8, 2048, V).clone() + anchor.to(torch.bfloat16)
+            got = []
+            logits.register_hook(lambda gr: got.append(gr))
+            loss = nmce.vocab_parallel_cross_entropy(logits, tv, 0, V, ctx, inplace=inplace,
+                                                     upstream_hint=hint)
+            (loss * upstream).backward()
+            assert loss.item() == loss2.item()
+            grad = got[0].view(N, V)
+            assert (grad.data_ptr() == logits.data_ptr()) == (inplace is None)
+            assert torch.equal(grad.view(torch.int16), ref_grad.view(torch.int16)), \
+                (upstream, inplace)
+            del logits, got, grad
+        if upstream == 1.0:
+            per_token = nmce._VocabParallelCrossEntropy.apply(x.view(8, 2048, V), tv, 0, V,
+                                                              None, 1, False)
+            assert_close_rel(per_token.reshape(-1).cpu().numpy(), ref_loss.cpu().numpy(), 1e-5,
+                             what="c2 loss")
+            assert abs(loss2.item() - ref_loss.mean().item()) <= 1e-6 * abs(
+                ref_loss.mean().item())
+            rs = ref_grad.float().sum(-1) * N
+            assert rs.abs().max().item() < 2e-2, rs.abs().max().item()
+            _, og = ce_oracle.closed_form(xs, ts, 1.0 / N)
+            assert_bf16_close(ref_grad[pick].float().cpu().numpy(), og, what="c2 grad rows",
+                              atol=1e-30)
+        del ref_grad
+    torch.cuda.empty_cache()
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -163,5 +163,3 @@ def test_one_pass_scaled_loss_replays_exactly():
         assert got[0] == le.item(), f"replay {rep}: loss {got[0]} vs eager {le.item()}"
         assert torch.equal(got[1].view(torch.int16), xe.grad.view(torch.int16)), \
             f"replay {rep}: gradient differs from the two-pass eager step"
-    from nmce import cross_entropy as ce
-    ce._hint(torch.device(DEV)).fill_(1.0)

@@ -613,14 +613,18 @@ def _lse_all(xd, wd, chunk=1024):
     return torch.cat(out)
 
 
+@pytest.mark.parametrize("route", ["library", "nmce"])
 @pytest.mark.parametrize("cfg", ["c4", "c5"])
-def test_fused_workload(cfg):
+def test_fused_workload(cfg, route, monkeypatch):
     """c4: hidden [16384, 4096] ~ N(0,1), W [128256, 4096] ~ N(0, 0.02^2), uniform
     targets. c5: hidden [16384, 3072], W [256000, 3072] ~ N(0, 0.05^2) with 64
-    rows x30, Zipf(1.1) targets (logits far beyond +-60)."""
+    rows x30, Zipf(1.1) targets (logits far beyond +-60). Both backward
+    routes: the library's products, and the hand-written one with dX
+    accumulated in fp32 over the 32768-row vocabulary chunks (4 at c4, 8 at
+    c5)."""
     import nmce
-    from nmce import _lib as L
-    lib = L.load()
+    from nmce import lmhead as lm
+    monkeypatch.setattr(lm, "BACKWARD_GEMM", route)
     g = torch.Generator(device=DEV).manual_seed(0)
     if cfg == "c4":
         n, h, v = 16384, 4096, 128256
@@ -637,7 +641,7 @@ def test_fused_workload(cfg):
         del wf
         ranks = torch.arange(1, v + 1, device=DEV, dtype=torch.float64)
         t = torch.multinomial((ranks ** -1.1).float(), n, replacement=True, generator=g)
-    print(f"[fused-workload] {cfg} n={n} h={h} v={v}", flush=True)
+    print(f"[fused-workload] {cfg} n={n} h={h} v={v} backward {route}", flush=True)
     ctx = nmce.ParallelContext.single()
     xd = x.clone().requires_grad_(True)
     wd = w.clone().requires_grad_(True)
