@@ -41,6 +41,7 @@ extern "C" {
 #define NMCE_EINVAL_PTR (-4)
 #define NMCE_EINVAL_TP (-5)
 #define NMCE_EINVAL_WORKSPACE (-6)
+#define NMCE_EINVAL_SCRATCH (-7)
 
 /* Rows covered by one int32 count of nmce_validate_targets. */
 #define NMCE_VALIDATE_ROWS_PER_SLOT 1024
@@ -251,6 +252,25 @@ int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, 
                              int64_t vocab_start, float* row_max, float* row_sumexp_m1,
                              float* target_logit, void* workspace, int64_t workspace_bytes,
                              void* stream);
+
+/*
+ * nmce_lmhead_ce_fwd_stats without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The partial statistics go to a fixed 64 MiB device array inside the
+ * library (one per GPU, held until the process ends), and the tokens are
+ * processed in as many launches as it takes to fit them there; the results
+ * are bit-identical to nmce_lmhead_ce_fwd_stats. The call allocates nothing.
+ * Limit: 3 * ceil(vocab_local / 128) * 4 bytes per token must fit in 64 MiB
+ * (vocab_local up to 715,827,840); beyond that it returns
+ * NMCE_EINVAL_SCRATCH before launching anything. Every call on one GPU uses
+ * the same array: calls that overlap on one GPU (different streams, or
+ * threads) race and must be serialised by the caller.
+ */
+int nmce_lmhead_ce_fwd_stats_noalloc(const void* hidden, const void* weight, int dtype,
+                                     int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                     const int64_t* target, int64_t vocab_start, float* row_max,
+                                     float* row_sumexp_m1, float* target_logit, void* stream);
 
 /* Device workspace bytes needed by nmce_lmhead_ce_bwd for a vocabulary chunk
  * of vocab_chunk rows (<= 0: the whole shard in one chunk). */

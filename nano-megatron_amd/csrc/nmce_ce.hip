@@ -656,6 +656,8 @@ const char* nmce_status_string(int status) {
     case NMCE_EINVAL_PTR: return "null pointer for a required argument";
     case NMCE_EINVAL_TP: return "tensor-parallel size must be >= 1";
     case NMCE_EINVAL_WORKSPACE: return "workspace too small or misaligned";
+    case NMCE_EINVAL_SCRATCH:
+      return "the problem does not fit the fixed scratch of the allocation-free entry point";
     default:
       return status > 0 ? hipGetErrorString(static_cast<hipError_t>(status)) : "unknown status";
   }

@@ -41,6 +41,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 
 #include "nmce.h"
 #include "nmce_device.h"
@@ -706,6 +708,72 @@ BwdLayout bwd_layout(int64_t n, int64_t h, int64_t v, int64_t chunk) {
 
 int64_t fwd_partial_blocks(int64_t v) { return (v + kPartialRows - 1) / kPartialRows; }
 
+int check_fwd_args(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                   int64_t hidden_size, int64_t vocab_local, const int64_t* target,
+                   const float* row_max, const float* row_sumexp_m1, const float* target_logit) {
+  if (dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
+  if (n_rows < 0 || vocab_local < 1 || hidden_size < kBK || hidden_size % kBK != 0)
+    return NMCE_EINVAL_SHAPE;
+  if (n_rows == 0) return NMCE_OK;
+  if (!operand_ok(hidden, hidden_size) || !operand_ok(weight, hidden_size))
+    return NMCE_EINVAL_ALIGN;
+  if (!target || !row_max || !row_sumexp_m1 || !target_logit) return NMCE_EINVAL_PTR;
+  if (n_rows > (int64_t{1} << 30) || vocab_local > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
+  return NMCE_OK;
+}
+
+// The statistics GEMM over n tokens and its reduction, with the
+// [3, fwd_partial_blocks(V), n] fp32 partials at `partials`.
+int launch_fwd_stats(const uint16_t* X, const uint16_t* W, int64_t n, int64_t H, int64_t V,
+                     const int64_t* target, int64_t vstart, float* row_max, float* row_sumexp_m1,
+                     float* target_logit, float* partials, hipStream_t s) {
+  const int64_t nb = fwd_partial_blocks(V);
+  float* pmax = partials;
+  float* psum1 = pmax + nb * n;
+  float* ptgt = psum1 + nb * n;
+  const int64_t tiles = ((V + kBM - 1) / kBM) * ((n + kBN - 1) / kBN);
+  hipLaunchKernelGGL(lmhead_stats_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
+                     kLdsBytes, s, W, X, V, n, H, target, vstart, pmax, psum1, ptgt);
+  int st = launch_status();
+  if (st) return st;
+  hipLaunchKernelGGL(lmhead_reduce_partials_kernel,
+                     dim3(static_cast<unsigned>((n + kRedTokens - 1) / kRedTokens)),
+                     dim3(kRedTokens * kRedSlices), 0, s, pmax, psum1, ptgt, nb, n, row_max,
+                     row_sumexp_m1, target_logit);
+  return launch_status();
+}
+
+// ---- the allocation-free forward's scratch ----------------------------------
+// The partial statistics of nmce_lmhead_ce_fwd_stats_noalloc live in this
+// fixed device array (one copy per GPU, held until the process ends) instead
+// of a caller workspace. In host code `scratch` only names the array: its
+// device address on the current GPU comes from hipGetSymbolAddress, taken once
+// per device and kept in scratch_ptr.
+constexpr int64_t kScratchBytes = int64_t{64} << 20;
+constexpr int64_t kScratchFloats = kScratchBytes / 4;
+static __device__ __align__(256) float scratch[kScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mu;
+float* scratch_ptr[kMaxDevices] = {};
+
+int scratch_on_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return static_cast<int>(e);
+  if (dev < 0 || dev >= kMaxDevices) return NMCE_EINVAL_SCRATCH;
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (!scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return static_cast<int>(e);
+    if (!p) return NMCE_EINVAL_SCRATCH;
+    scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = scratch_ptr[dev];
+  return NMCE_OK;
+}
+
 }  // namespace
 }  // namespace nmce
 
@@ -730,34 +798,44 @@ int nmce_lmhead_ce_fwd_stats(const void* hidden, const void* weight, int dtype, 
                              int64_t vocab_start, float* row_max, float* row_sumexp_m1,
                              float* target_logit, void* workspace, int64_t workspace_bytes,
                              void* stream) {
-  if (dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
-  if (n_rows < 0 || vocab_local < 1 || hidden_size < kBK || hidden_size % kBK != 0)
-    return NMCE_EINVAL_SHAPE;
-  if (n_rows == 0) return NMCE_OK;
-  if (!operand_ok(hidden, hidden_size) || !operand_ok(weight, hidden_size))
-    return NMCE_EINVAL_ALIGN;
-  if (!target || !row_max || !row_sumexp_m1 || !target_logit) return NMCE_EINVAL_PTR;
-  if (n_rows > (int64_t{1} << 30) || vocab_local > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
+  int st = check_fwd_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, target, row_max,
+                          row_sumexp_m1, target_logit);
+  if (st != NMCE_OK || n_rows == 0) return st;
   const int64_t need = nmce_lmhead_ce_fwd_workspace_bytes(n_rows, hidden_size, vocab_local);
   if (!workspace || workspace_bytes < need || !aligned16(workspace)) return NMCE_EINVAL_WORKSPACE;
-  int st = configure_lds();
-  if (st) return st;
-  auto s = static_cast<hipStream_t>(stream);
-  const int64_t nb = fwd_partial_blocks(vocab_local);
-  float* pmax = static_cast<float*>(workspace);
-  float* psum1 = pmax + nb * n_rows;
-  float* ptgt = psum1 + nb * n_rows;
-  const int64_t tiles = ((vocab_local + kBM - 1) / kBM) * ((n_rows + kBN - 1) / kBN);
-  hipLaunchKernelGGL(lmhead_stats_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
-                     kLdsBytes, s, static_cast<const uint16_t*>(weight),
-                     static_cast<const uint16_t*>(hidden), vocab_local, n_rows, hidden_size,
-                     target, vocab_start, pmax, psum1, ptgt);
-  if ((st = launch_status())) return st;
-  hipLaunchKernelGGL(lmhead_reduce_partials_kernel,
-                     dim3(static_cast<unsigned>((n_rows + kRedTokens - 1) / kRedTokens)),
-                     dim3(kRedTokens * kRedSlices), 0, s, pmax, psum1, ptgt, nb, n_rows, row_max,
-                     row_sumexp_m1, target_logit);
-  return launch_status();
+  if ((st = configure_lds())) return st;
+  return launch_fwd_stats(static_cast<const uint16_t*>(hidden), static_cast<const uint16_t*>(weight),
+                          n_rows, hidden_size, vocab_local, target, vocab_start, row_max,
+                          row_sumexp_m1, target_logit, static_cast<float*>(workspace),
+                          static_cast<hipStream_t>(stream));
+}
+
+int nmce_lmhead_ce_fwd_stats_noalloc(const void* hidden, const void* weight, int dtype,
+                                     int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                     const int64_t* target, int64_t vocab_start, float* row_max,
+                                     float* row_sumexp_m1, float* target_logit, void* stream) {
+  int st = check_fwd_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, target, row_max,
+                          row_sumexp_m1, target_logit);
+  if (st != NMCE_OK || n_rows == 0) return st;
+  // Tokens per launch: as many as the scratch holds the partials of, in
+  // whole 256-token tile columns when that is at least one column.
+  const int64_t per_token = 3 * fwd_partial_blocks(vocab_local);  // floats
+  if (per_token > kScratchFloats) return NMCE_EINVAL_SCRATCH;
+  int64_t chunk = kScratchFloats / per_token;
+  if (chunk >= kBN) chunk = chunk / kBN * kBN;
+  float* partials = nullptr;
+  if ((st = scratch_on_current_device(&partials))) return st;
+  if ((st = configure_lds())) return st;
+  const auto* X = static_cast<const uint16_t*>(hidden);
+  for (int64_t t0 = 0; t0 < n_rows; t0 += chunk) {
+    const int64_t m = (n_rows - t0) < chunk ? (n_rows - t0) : chunk;
+    st = launch_fwd_stats(X + t0 * hidden_size, static_cast<const uint16_t*>(weight), m,
+                          hidden_size, vocab_local, target + t0, vocab_start, row_max + t0,
+                          row_sumexp_m1 + t0, target_logit + t0, partials,
+                          static_cast<hipStream_t>(stream));
+    if (st) return st;
+  }
+  return NMCE_OK;
 }
 
 }  // extern "C"

@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple] = {
     "nmce_lmhead_ce_fwd_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "nmce_lmhead_ce_fwd_stats": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p,
                                           _p, _i64, _p]),
+    "nmce_lmhead_ce_fwd_stats_noalloc": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p,
+                                                  _p, _p, _p]),
     "nmce_lmhead_ce_bwd_workspace_bytes": (_i64, [_i64, _i64, _i64, _i64]),
     "nmce_lmhead_ce_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64,
                                     _p, _p, _i64, _p, _i64, _p]),
