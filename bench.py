@@ -104,6 +104,10 @@ def parse_args():
     p.add_argument("--fused-warmup", type=int, default=2)
     p.add_argument("--vocab-chunk", type=int, default=None,
                    help="fused backward: vocabulary rows per chunk (default: the library's)")
+    p.add_argument("--token-chunk", type=int, default=None,
+                   help="fused one-pass path: tokens per chunk (default: the library's)")
+    p.add_argument("--fused-two-pass", action="store_true",
+                   help="fused workloads: the recomputing backward (one_pass=False)")
     return p.parse_args()
 
 
@@ -260,7 +264,7 @@ def cpu_baseline_fused(wl: dict, seconds: float, rows: int = 128) -> dict:
     }
 
 
-def _kernel_times(step, steps: int) -> dict:
+def _kernel_times(step, steps: int, with_counts: bool = False):
     """Average duration per launch of each libnmce kernel over ``steps`` more
     steps, from HIP event pairs recorded on the launch stream around every
     launch (nmce.cross_entropy.kernel_timeline). Event records add small gaps
@@ -279,7 +283,10 @@ def _kernel_times(step, steps: int) -> dict:
     per: dict[str, list[float]] = {}
     for name, s_ev, e_ev in timeline:
         per.setdefault(name, []).append(s_ev.elapsed_time(e_ev))
-    return {k: sum(vs) / len(vs) for k, vs in per.items()}
+    avg = {k: sum(vs) / len(vs) for k, vs in per.items()}
+    if with_counts:
+        return avg, {k: len(vs) for k, vs in per.items()}
+    return avg
 
 
 def fused_inputs(wl: dict, dev):
@@ -321,7 +328,9 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
         xp.grad = None  # zero_grad(set_to_none=True) between steps
         wp.grad = None
         loss = nmce.lmhead_vocab_parallel_cross_entropy(xp, wp, t, 0, v, ctx,
-                                                        vocab_chunk=args.vocab_chunk)
+                                                        vocab_chunk=args.vocab_chunk,
+                                                        token_chunk=args.token_chunk,
+                                                        one_pass=not args.fused_two_pass)
         loss.backward()
         return loss
 
@@ -333,7 +342,7 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
         step()
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
-    avg_ms = _kernel_times(step, steps)
+    avg_ms, counts = _kernel_times(step, steps, with_counts=True)
 
     calib = None
     if args.calibrate_copy:
@@ -347,11 +356,18 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
         calib = w.numel() * 2
         del dst
 
-    gemm_flops = 2.0 * n * v * h
-    dominant = "nmce_lmhead_ce_fwd_stats"
-    achieved = gemm_flops / (avg_ms[dominant] * 1e-3) / 1e12
+    gemm_flops = 2.0 * n * v * h   # one product over every token
+    one_pass = "nmce_lmhead_ce_fused_chunk_stats" in avg_ms
+    # The statistics GEMM: on the one-pass path one launch per token chunk
+    # (the GEMM that keeps the exponentials, plus the small reduction of its
+    # partials), else one launch over every token.
+    dominant = "nmce_lmhead_ce_fused_chunk_stats" if one_pass else "nmce_lmhead_ce_fwd_stats"
+    per_step = counts[dominant] / steps
+    flops_per_launch = gemm_flops / per_step
+    achieved = flops_per_launch / (avg_ms[dominant] * 1e-3) / 1e12
     alg_flops = 3 * gemm_flops      # forward GEMM + the dX and dW GEMMs
-    exe_flops = 4 * gemm_flops      # plus the recomputation of the logits in backward
+    # the recomputing backward also recomputes the logits
+    exe_flops = alg_flops if one_pass else 4 * gemm_flops
     result = {
         "metric": METRIC,
         "value": n / (ms_per_step * 1e-3),
@@ -371,8 +387,14 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
             "hidden": h,
             "vocab_local": v,
             "tp": 1,
-            "path": "nmce.lmhead_vocab_parallel_cross_entropy fwd+bwd (logits never stored; "
-                    "bf16 MFMA, fp32 accumulate), target validation, dX and dW",
+            "path": ("nmce.lmhead_vocab_parallel_cross_entropy fwd+bwd, one pass: per chunk "
+                     "of tokens the statistics GEMM keeps its exponentials, dZ follows from "
+                     "them, dX and dW by libnmce's GEMM (logits computed once, never stored "
+                     "whole; bf16 MFMA, fp32 accumulate), target validation"
+                     if one_pass else
+                     "nmce.lmhead_vocab_parallel_cross_entropy fwd+bwd (logits never stored; "
+                     "recomputed by vocabulary chunk in the backward; bf16 MFMA, fp32 "
+                     "accumulate), target validation, dX and dW"),
         },
         "roofline": {
             "bound": "mfma",
@@ -382,8 +404,9 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
             "traffic": measured_traffic(name, "lmhead_stats_kernel", LMHEAD_TRAFFIC_FILE),
-            "alg_flops_per_launch": gemm_flops,
+            "alg_flops_per_launch": flops_per_launch,
             "avg_launch_ms": avg_ms[dominant],
+            "launches_per_step": per_step,
         },
         "kernels_ms": avg_ms,
         "path_roofline": {

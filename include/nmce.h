@@ -341,6 +341,82 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
                        void* grad_weight, int64_t vocab_chunk, void* workspace,
                        int64_t workspace_bytes, void* stream);
 
+/* ---------------------------------------------------------------------------
+ * One-pass fused LM head + loss: forward and backward in the forward, for
+ * the upstream value the caller assumes (bf16 only; same operand layout as
+ * above). The tokens go in chunks of token_chunk (rounded up to 256; <= 0:
+ * all at once). Per chunk the statistics GEMM keeps its exponentials
+ * P = exp(z - block max) in the workspace; once the chunk's statistics are
+ * combined across the TP group, dZ follows from P by one factor per
+ * (128-row block, token), and the dX rows of the chunk and its share of dW
+ * are formed by libnmce's GEMM. Nothing of size [n_rows, vocab_local] exists
+ * (a chunk's P and dZ are [token_chunk, vocab_local]), and the logits are
+ * computed once: 6 * n_rows * vocab_local * hidden_size flops in all.
+ * Replaces model.py:192 followed by cross_entropy.py:17-65 and the matmul
+ * backward of model.py:192; with a caller that assumes the right upstream
+ * value, as the reference's forward computes the softmax its backward
+ * returns (cross_entropy.py:48-49).
+ * --------------------------------------------------------------------------- */
+
+/*
+ * Workspace layout (int64 values) written to layout[0 .. 11]:
+ *   [0] total bytes  [1] chunk (tokens per chunk)  [2] n_chunks
+ *   [3] ldt (chunk padded to 64)  [4] vpad (vocab_local padded to 256)
+ *   [5] nb (ceil(vocab_local / 128))  [6..11] byte offsets of W^T, X_c^T,
+ *   P^T (= dZ_c^T), dZ_c, the partial statistics and the fp32 dW
+ *   accumulator (present when n_chunks > 1).
+ */
+#define NMCE_LMHEAD_FUSED_LAYOUT_FIELDS 12
+int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                int64_t token_chunk, int64_t* layout);
+
+/* assumed[0] = hint[0], or 1.0 when hint[0] is zero, subnormal, infinite or
+ * NaN (a gradient written for such a value could not be rescaled). Both are
+ * device pointers to one float. */
+int nmce_hint_assume(const float* hint, float* assumed, void* stream);
+
+/* Once per forward, before the chunks: W^T into the workspace. */
+int nmce_lmhead_ce_fused_prepare(const void* hidden, const void* weight, int dtype,
+                                 int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                 int64_t token_chunk, void* workspace, int64_t workspace_bytes,
+                                 void* stream);
+
+/*
+ * Chunk c (tokens [c*chunk, min((c+1)*chunk, n_rows))): this shard's
+ * statistics of those tokens, as nmce_lmhead_ce_fwd_stats computes them,
+ * written at the tokens' positions of row_max / row_sumexp_m1 /
+ * target_logit ([n_rows] each), and P of the chunk kept in the workspace.
+ * Chunks run in order 0, 1, ..., each followed by its
+ * nmce_lmhead_ce_fused_chunk_grads.
+ */
+int nmce_lmhead_ce_fused_chunk_stats(const void* hidden, const void* weight, int dtype,
+                                     int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                     const int64_t* target, int64_t vocab_start,
+                                     int64_t token_chunk, int64_t chunk_index, float* row_max,
+                                     float* row_sumexp_m1, float* target_logit, void* workspace,
+                                     int64_t workspace_bytes, void* stream);
+
+/*
+ * Chunk c's gradients, given the combined statistics g_max / g_sumexp_m1 of
+ * its tokens (nmce_ce_combine over the TP group) and this shard's
+ * target_logit from nmce_lmhead_ce_fused_chunk_stats:
+ *   dZ[t, v]          = (softmax - onehot) * grad_output[t*gout_stride] / gout_div
+ *                       (target column as in nmce_ce_bwd), rounded to bf16
+ *   grad_hidden rows  = dZ_c @ weight                 (this shard's share)
+ *   grad_weight      += dZ_c^T @ hidden_c             (fp32 across chunks,
+ *                       bf16 when the last chunk is done)
+ * grad_hidden is [n_rows, hidden_size], grad_weight [vocab_local,
+ * hidden_size], both bf16.
+ */
+int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int dtype,
+                                     int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                     const int64_t* target, int64_t vocab_start,
+                                     int64_t token_chunk, int64_t chunk_index, const float* g_max,
+                                     const float* g_sumexp_m1, const float* target_logit,
+                                     const float* grad_output, int64_t gout_stride,
+                                     float gout_div, void* grad_hidden, void* grad_weight,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
+
 /*
  * The GEMM core of the fused path, exposed for testing and measurement (no
  * counterpart in the reference): c[i, j] = sum_l a[i, l] * b[j, l] for

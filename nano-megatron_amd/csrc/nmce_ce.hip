@@ -243,16 +243,6 @@ __global__ __launch_bounds__(kValidateThreads) void validate_targets_kernel(
   }
 }
 
-// The target column's gradient, (softmax - 1) * g with softmax =
-// exp(x - M) / (1 + T1). When the target is the maximum this is
-// -T1 / (1 + T1) * g, formed from T1 itself: for a confident token it keeps
-// full relative precision instead of being the difference of two numbers
-// near 1. Otherwise the maximum's own 1 is part of 1 + T1 as well as the
-// target's term, so the softmax is at most 1/2 and softmax - 1 loses nothing.
-__device__ __forceinline__ float target_grad(float x, float M, float T1, float g) {
-  const float S = 1.0f + T1;
-  return x == M ? -T1 / S * g : (exp_shift(x, M) / S - 1.0f) * g;
-}
 
 // Replace y[d] by the target column's gradient when 0 <= d < K, with px the
 // vector's first logit. The target's logit is read again from px[d] (the
@@ -405,15 +395,6 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
     set_target<EPV>(y, x + row * ld + cols[u], d, M, T1, go);
     store_stream(reinterpret_cast<u32x4*>(g + row * ldg + cols[u]), E::pack(y));
   }
-}
-
-// The upstream value a one-pass forward computes the gradient for: the hint,
-// or 1.0 (loss.backward()'s value) when the hint is zero, subnormal, infinite
-// or NaN. A gradient written for such a value could not be rescaled to the
-// real one, which the in-place form relies on after a miss.
-__device__ __forceinline__ float usable_hint(float h) {
-  const float a = fabsf(h);
-  return (a >= FLT_MIN && a <= FLT_MAX) ? h : 1.0f;
 }
 
 // Forward and backward of whole-vocabulary rows (TP = 1) in one read of the

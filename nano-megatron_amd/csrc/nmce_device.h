@@ -52,6 +52,26 @@ __device__ __forceinline__ void merge_excess(float& m, float& t, float m2, float
   t = fmaf(1.0f + small_t, exp_shift(small_m, m), big_t);
 }
 
+// The target column's gradient, (softmax - 1) * g with softmax =
+// exp(x - M) / (1 + T1). When the target is the maximum this is
+// -T1 / (1 + T1) * g, formed from T1 itself: for a confident token it keeps
+// full relative precision instead of being the difference of two numbers
+// near 1. Otherwise the maximum's own 1 is part of 1 + T1 as well as the
+// target's term, so the softmax is at most 1/2 and softmax - 1 loses nothing.
+__device__ __forceinline__ float target_grad(float x, float M, float T1, float g) {
+  const float S = 1.0f + T1;
+  return x == M ? -T1 / S * g : (exp_shift(x, M) / S - 1.0f) * g;
+}
+
+// The upstream value a one-pass forward computes the gradient for: the hint,
+// or 1.0 (loss.backward()'s value) when the hint is zero, subnormal, infinite
+// or NaN. A gradient written for such a value could not be rescaled to the
+// real one, which the in-place forms rely on after a miss.
+__device__ __forceinline__ float usable_hint(float h) {
+  const float a = fabsf(h);
+  return (a >= 1.17549435e-38f && a <= 3.40282347e+38f) ? h : 1.0f;
+}
+
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) {

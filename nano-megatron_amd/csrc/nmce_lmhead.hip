@@ -565,6 +565,205 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// One-pass fused loss, step 1 (per chunk of tokens): the statistics GEMM of
+// lmhead_stats_kernel whose epilogue also keeps the exponentials it forms,
+//   pt[v * ldt + t] = bf16(exp(z[v, t] - pmax[b * N + t]))   (b = v / 128)
+// for v < V and t < N, and 0 for the padding of the tile grid (rows up to the
+// next multiple of 256, tokens up to ldt). Once the row statistics are known,
+// dZ is pt times one factor per (block, token) (lmhead_dz_rescale_kernel), so
+// the logits never need to be recomputed. pt leaves through LDS as 512-byte
+// row segments, as in lmhead_dz_kernel.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
+    const uint16_t* __restrict__ W, const uint16_t* __restrict__ X, int64_t V, int64_t N,
+    int64_t H, const int64_t* __restrict__ target, int64_t vstart, float* __restrict__ pmax,
+    float* __restrict__ psum1, float* __restrict__ ptgt, uint16_t* __restrict__ pt,
+    int64_t ldt) {
+  extern __shared__ __align__(16) char lds[];
+  const int tiles_m = static_cast<int>((V + kBM - 1) / kBM);
+  const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
+  int tm, tn;
+  tile_coords<kGroupMStats>(tiles_m, tiles_n, tm, tn);
+  const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
+  Acc acc;
+  gemm_mainloop(W, H, V, X, H, N, H, m0, n0, lds, acc);
+
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int fhalf = lane >> 5;
+  const int64_t vrow0 = m0 + wm * kWaveM;  // first vocabulary row of this wave
+  const int64_t blk = vrow0 / kPartialRows;
+  const int64_t vr = V - vrow0;
+  // rows >= valid_rows of this wave's 128 are padding (possibly all of them)
+  const int valid_rows = static_cast<int>(vr < 0 ? 0 : (vr < kWaveM ? vr : kWaveM));
+  __syncthreads();  // every wave is done with the operand buffers
+  uint32_t* P = reinterpret_cast<uint32_t*>(lds);
+  auto pcol = [](int vp, int t) { return t ^ (((vp >> 2) & 15) << 2); };
+#pragma unroll
+  for (int fn = 0; fn < kFN; ++fn) {
+    const int tloc = wn * kWaveN + 32 * fn + (lane & 31);
+    const int64_t tok = n0 + tloc;
+    const bool tok_ok = tok < N;
+    int tl = -1;  // target row within this wave's valid rows, or -1
+    if (tok_ok) {
+      const int64_t t = target[tok] - vstart - vrow0;
+      tl = (t >= 0 && t < valid_rows) ? static_cast<int>(t) : -1;
+    }
+    float mx = kMaxFloorL;
+    float pick = 0.0f;
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = acc_row(fm, e, fhalf);
+        const float z = acc.c[fm][fn][e];
+        if (r < valid_rows) mx = fmaxf(mx, z);
+        pick = (r == tl) ? z : pick;
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    // sum exp(z - mx) - 1 with the terms equal to 1 counted apart (as in
+    // lmhead_stats_kernel); each exponential also goes to the LDS tile.
+    float se = 0.0f, sr = 0.0f;
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm) {
+      float d[16];
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int r = acc_row(fm, e, fhalf);
+        const float p = r < valid_rows ? exp_shift(acc.c[fm][fn][e], mx) : 0.0f;
+        se += p;
+        sr += __builtin_amdgcn_fractf(p);
+        d[e] = tok_ok ? p : 0.0f;
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int vp = (wm * kWaveM + 32 * fm + 8 * q + 4 * fhalf) >> 1;
+        const int col = pcol(vp, tloc);
+        P[vp * kBN + col] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
+        P[(vp + 1) * kBN + col] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
+      }
+    }
+    se += __shfl_xor(se, 32);
+    sr += __shfl_xor(sr, 32);
+    pick += __shfl_xor(pick, 32);
+    const float ones = rintf(se - sr);
+    if (fhalf == 0 && tok_ok && valid_rows > 0) {
+      pmax[blk * N + tok] = mx;
+      psum1[blk * N + tok] = (ones - 1.0f) + sr;
+      ptgt[blk * N + tok] = pick;
+    }
+  }
+  __syncthreads();
+  // pt [Mpad, ldt]: 32 lanes cover one pair of vocabulary rows (256 tokens).
+#pragma unroll 2
+  for (int it = 0; it < (kBM / 2) * (kBN / 8) / kThreads; ++it) {
+    const int lin = it * kThreads + static_cast<int>(threadIdx.x);
+    const int vp = lin / (kBN / 8);
+    const int t0 = 8 * (lin % (kBN / 8));
+    const u32x4 a = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, t0));
+    const u32x4 b = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, t0 + 4));
+    const u32x4 lo = {(a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
+                      (b.x & 0xffffu) | (b.y << 16), (b.z & 0xffffu) | (b.w << 16)};
+    const u32x4 hi = {(a.x >> 16) | (a.y & 0xffff0000u), (a.z >> 16) | (a.w & 0xffff0000u),
+                      (b.x >> 16) | (b.y & 0xffff0000u), (b.z >> 16) | (b.w & 0xffff0000u)};
+    const int64_t tok0 = n0 + t0;
+    if (tok0 < ldt) {
+      *reinterpret_cast<u32x4*>(pt + (m0 + 2 * vp) * ldt + tok0) = lo;
+      *reinterpret_cast<u32x4*>(pt + (m0 + 2 * vp + 1) * ldt + tok0) = hi;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// One-pass fused loss, step 2: dZ from the kept exponentials, once the row
+// statistics (M, T1) are combined (cross_entropy.py:53-65):
+//   dZ[t, v] = exp(z - M) / (1 + T1) * g = pt[v, t] * exp(pmax[b, t] - M) * g / (1 + T1)
+// and, on the target row, (softmax - 1) * g from the fp32 target logit
+// (target_grad). Written in place into pt (vocabulary-major, the dW GEMM's A)
+// and transposed into dz [N, ldz] (token-major, the dX GEMM's A). A workgroup
+// takes one 128-row block of partial statistics and 64 tokens; the factor of
+// each (block, token) is formed once. Rows past V and blocks past nb come out
+// 0 (pt holds 0 there), tokens past N are not written to dz.
+// ---------------------------------------------------------------------------
+constexpr int kRsRows = kPartialRows;  // 128: one block of partial statistics
+constexpr int kRsToks = 64;
+
+__global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
+    uint16_t* __restrict__ pt, int64_t ldt, uint16_t* __restrict__ dz, int64_t ldz, int64_t V,
+    int64_t N, const float* __restrict__ pmax, int64_t nb, const float* __restrict__ gmax,
+    const float* __restrict__ gsum1, const float* __restrict__ tlogit,
+    const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ gout,
+    int64_t gstride, float gdiv) {
+  __shared__ float s_scale[kRsToks];
+  __shared__ float s_dt[kRsToks];
+  __shared__ int s_tv[kRsToks];
+  // token-major copy of the tile for the dz stores; rows padded by 16 bytes
+  __shared__ __align__(16) uint16_t tile[kRsToks][kRsRows + 8];
+  const int64_t blk = blockIdx.x;
+  const int64_t v0 = blk * kRsRows;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kRsToks;
+  const int tid = threadIdx.x;
+  if (tid < kRsToks) {
+    const int64_t t = t0 + tid;
+    float c = 0.0f, dt = 0.0f;
+    int tv = -1;
+    if (t < N && blk < nb) {
+      const float M = gmax[t], T1 = gsum1[t];
+      const float g = gout[t * gstride] / gdiv;
+      c = exp_shift(pmax[blk * N + t], M) * (g / (1.0f + T1));
+      const int64_t lt = target[t] - vstart - v0;
+      if (lt >= 0 && lt < kRsRows && v0 + lt < V) {
+        tv = static_cast<int>(lt);
+        dt = target_grad(tlogit[t], M, T1, g);
+      }
+    }
+    s_scale[tid] = c;
+    s_dt[tid] = dt;
+    s_tv[tid] = tv;
+  }
+  __syncthreads();
+  // pt: 128 rows x 64 tokens, 8 vectors of 8 tokens per row.
+#pragma unroll
+  for (int it = 0; it < kRsRows * (kRsToks / 8) / 256; ++it) {
+    const int lin = it * 256 + tid;
+    const int r = lin / (kRsToks / 8);
+    const int tg = 8 * (lin % (kRsToks / 8));
+    u32x4* p = reinterpret_cast<u32x4*>(pt + (v0 + r) * ldt + t0 + tg);
+    float f[8];
+    Elem<uint16_t>::unpack(*p, f);
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      // A zero factor (padding, or an exponential that underflows) writes 0
+      // whatever the buffer held: the padding columns past a short last
+      // chunk's tiles were never written.
+      const float c = s_scale[tg + k];
+      f[k] = c == 0.0f ? 0.0f : f[k] * c;
+      f[k] = (s_tv[tg + k] == r) ? s_dt[tg + k] : f[k];
+    }
+    const u32x4 w = Elem<uint16_t>::pack(f);
+    *p = w;
+    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      tile[tg + 2 * k][r] = static_cast<uint16_t>(ws[k] & 0xffffu);
+      tile[tg + 2 * k + 1][r] = static_cast<uint16_t>(ws[k] >> 16);
+    }
+  }
+  __syncthreads();
+  // dz: 64 token rows x 128 vocabulary entries, 16 vectors per row.
+#pragma unroll
+  for (int it = 0; it < kRsToks * (kRsRows / 8) / 256; ++it) {
+    const int lin = it * 256 + tid;
+    const int t = lin / (kRsRows / 8);
+    const int vg = 8 * (lin % (kRsRows / 8));
+    if (t0 + t < N)
+      *reinterpret_cast<u32x4*>(dz + (t0 + t) * ldz + v0 + vg) =
+          *reinterpret_cast<const u32x4*>(&tile[t][vg]);
+  }
+}
+
 // bf16 transpose with zero padding: out[c * ldo + r] = in[r * ldi + c] for
 // r < R, c < C; out[c * ldo + r] = 0 for R <= r < ldo. 64x64 tiles through
 // LDS; interior tiles move 16 bytes per load and per store (ldi, ldo and the
@@ -635,6 +834,7 @@ int configure_lds() {
   const void* kernels[] = {
       reinterpret_cast<const void*>(&lmhead_stats_kernel),
       reinterpret_cast<const void*>(&lmhead_dz_kernel),
+      reinterpret_cast<const void*>(&lmhead_p_kernel),
       reinterpret_cast<const void*>(&gemm_store_kernel<0>),
       reinterpret_cast<const void*>(&gemm_store_kernel<1>),
       reinterpret_cast<const void*>(&gemm_store_kernel<2>),
@@ -707,6 +907,35 @@ BwdLayout bwd_layout(int64_t n, int64_t h, int64_t v, int64_t chunk) {
 }
 
 int64_t fwd_partial_blocks(int64_t v) { return (v + kPartialRows - 1) / kPartialRows; }
+
+// Workspace of the one-pass fused loss (all offsets 256-byte aligned).
+struct FusedLayout {
+  int64_t chunk;     // tokens per chunk (the last one may hold fewer)
+  int64_t n_chunks;
+  int64_t ldt;       // chunk tokens padded to 64: row stride of P^T and X^T, K of the dW GEMM
+  int64_t vpad;      // vocabulary padded to 256: rows of P^T, K of the dX GEMM
+  int64_t nb;        // 128-row blocks of partial statistics
+  int64_t off_wt, off_xt, off_pt, off_dz, off_part, off_acc, total;
+};
+
+FusedLayout fused_layout(int64_t n, int64_t h, int64_t v, int64_t token_chunk) {
+  FusedLayout L{};
+  L.chunk = (token_chunk <= 0 || token_chunk >= n) ? n : round_up(token_chunk, kBN);
+  if (L.chunk > n) L.chunk = n;
+  L.n_chunks = (n + L.chunk - 1) / L.chunk;
+  L.ldt = round_up(L.chunk, 64);
+  L.vpad = round_up(v, kBM);
+  L.nb = fwd_partial_blocks(v);
+  int64_t off = 0;
+  L.off_wt = off; off += align256(h * L.vpad * 2);
+  L.off_xt = off; off += align256(h * L.ldt * 2);
+  L.off_pt = off; off += align256(L.vpad * L.ldt * 2);
+  L.off_dz = off; off += align256(L.chunk * L.vpad * 2);
+  L.off_part = off; off += align256(3 * L.nb * L.chunk * 4);
+  L.off_acc = off; off += L.n_chunks > 1 ? align256(v * h * 4) : 0;
+  L.total = off;
+  return L;
+}
 
 int check_fwd_args(const void* hidden, const void* weight, int dtype, int64_t n_rows,
                    int64_t hidden_size, int64_t vocab_local, const int64_t* target,
@@ -985,6 +1214,162 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
       return st;
   }
   return NMCE_OK;
+}
+
+}  // extern "C"
+
+namespace nmce {
+namespace {
+
+__global__ void hint_assume_kernel(const float* __restrict__ hint, float* __restrict__ assumed) {
+  if (threadIdx.x == 0) assumed[0] = usable_hint(hint[0]);
+}
+
+int check_fused_args(const void* hidden, const void* weight, int dtype, int64_t n_rows,
+                     int64_t hidden_size, int64_t vocab_local, int64_t token_chunk,
+                     const void* workspace, int64_t workspace_bytes, FusedLayout& L) {
+  if (dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
+  if (n_rows < 1 || vocab_local < 1 || hidden_size < kBK || hidden_size % kBK != 0)
+    return NMCE_EINVAL_SHAPE;
+  if (n_rows > (int64_t{1} << 30) || vocab_local > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
+  if (!operand_ok(hidden, hidden_size) || !operand_ok(weight, hidden_size))
+    return NMCE_EINVAL_ALIGN;
+  L = fused_layout(n_rows, hidden_size, vocab_local, token_chunk);
+  // 256 rows of every GEMM operand must span less than 4 GiB (32-bit offsets).
+  if (!operand_ok(weight, L.vpad) || L.ldt >= (int64_t{1} << 22)) return NMCE_EINVAL_SHAPE;
+  if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
+    return NMCE_EINVAL_WORKSPACE;
+  return NMCE_OK;
+}
+
+}  // namespace
+}  // namespace nmce
+
+extern "C" {
+
+int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                int64_t token_chunk, int64_t* layout) {
+  if (!layout) return NMCE_EINVAL_PTR;
+  if (n_rows < 1 || hidden_size < 1 || vocab_local < 1) return NMCE_EINVAL_SHAPE;
+  const FusedLayout L = fused_layout(n_rows, hidden_size, vocab_local, token_chunk);
+  const int64_t v[NMCE_LMHEAD_FUSED_LAYOUT_FIELDS] = {
+      L.total, L.chunk, L.n_chunks, L.ldt, L.vpad, L.nb, L.off_wt, L.off_xt, L.off_pt, L.off_dz,
+      L.off_part, L.off_acc};
+  for (int i = 0; i < NMCE_LMHEAD_FUSED_LAYOUT_FIELDS; ++i) layout[i] = v[i];
+  return NMCE_OK;
+}
+
+int nmce_hint_assume(const float* hint, float* assumed, void* stream) {
+  if (!hint || !assumed) return NMCE_EINVAL_PTR;
+  hipLaunchKernelGGL(hint_assume_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     hint, assumed);
+  return launch_status();
+}
+
+int nmce_lmhead_ce_fused_prepare(const void* hidden, const void* weight, int dtype,
+                                 int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                 int64_t token_chunk, void* workspace, int64_t workspace_bytes,
+                                 void* stream) {
+  FusedLayout L;
+  int st = check_fused_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, token_chunk,
+                            workspace, workspace_bytes, L);
+  if (st) return st;
+  char* ws = static_cast<char*>(workspace);
+  // W^T [H, vpad], zero beyond the shard's rows: the dX GEMM's B operand.
+  return launch_transpose(static_cast<const uint16_t*>(weight), vocab_local, hidden_size,
+                          hidden_size, reinterpret_cast<uint16_t*>(ws + L.off_wt), L.vpad,
+                          static_cast<hipStream_t>(stream));
+}
+
+int nmce_lmhead_ce_fused_chunk_stats(const void* hidden, const void* weight, int dtype,
+                                     int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                     const int64_t* target, int64_t vocab_start,
+                                     int64_t token_chunk, int64_t chunk_index, float* row_max,
+                                     float* row_sumexp_m1, float* target_logit, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+  FusedLayout L;
+  int st = check_fused_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, token_chunk,
+                            workspace, workspace_bytes, L);
+  if (st) return st;
+  if (!target || !row_max || !row_sumexp_m1 || !target_logit) return NMCE_EINVAL_PTR;
+  if (chunk_index < 0 || chunk_index >= L.n_chunks) return NMCE_EINVAL_SHAPE;
+  if ((st = configure_lds())) return st;
+  auto s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int64_t t0 = chunk_index * L.chunk;
+  const int64_t nc = (n_rows - t0) < L.chunk ? (n_rows - t0) : L.chunk;
+  const int64_t H = hidden_size, V = vocab_local;
+  float* pmax = reinterpret_cast<float*>(ws + L.off_part);
+  float* psum1 = pmax + L.nb * nc;
+  float* ptgt = psum1 + L.nb * nc;
+  const int64_t tiles = (L.vpad / kBM) * ((nc + kBN - 1) / kBN);
+  hipLaunchKernelGGL(lmhead_p_kernel, dim3(static_cast<unsigned>(tiles)), dim3(kThreads),
+                     kLdsBytes, s, static_cast<const uint16_t*>(weight),
+                     static_cast<const uint16_t*>(hidden) + t0 * H, V, nc, H, target + t0,
+                     vocab_start, pmax, psum1, ptgt, reinterpret_cast<uint16_t*>(ws + L.off_pt),
+                     L.ldt);
+  if ((st = launch_status())) return st;
+  hipLaunchKernelGGL(lmhead_reduce_partials_kernel,
+                     dim3(static_cast<unsigned>((nc + kRedTokens - 1) / kRedTokens)),
+                     dim3(kRedTokens * kRedSlices), 0, s, pmax, psum1, ptgt, L.nb, nc,
+                     row_max + t0, row_sumexp_m1 + t0, target_logit + t0);
+  return launch_status();
+}
+
+int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int dtype,
+                                     int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
+                                     const int64_t* target, int64_t vocab_start,
+                                     int64_t token_chunk, int64_t chunk_index, const float* g_max,
+                                     const float* g_sumexp_m1, const float* target_logit,
+                                     const float* grad_output, int64_t gout_stride,
+                                     float gout_div, void* grad_hidden, void* grad_weight,
+                                     void* workspace, int64_t workspace_bytes, void* stream) {
+  FusedLayout L;
+  int st = check_fused_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, token_chunk,
+                            workspace, workspace_bytes, L);
+  if (st) return st;
+  if (!target || !g_max || !g_sumexp_m1 || !target_logit || !grad_output || !grad_hidden ||
+      !grad_weight)
+    return NMCE_EINVAL_PTR;
+  if (chunk_index < 0 || chunk_index >= L.n_chunks || gout_stride < 0 || !(gout_div > 0.0f))
+    return NMCE_EINVAL_SHAPE;
+  if ((st = configure_lds())) return st;
+  auto s = static_cast<hipStream_t>(stream);
+  char* ws = static_cast<char*>(workspace);
+  const int64_t t0 = chunk_index * L.chunk;
+  const int64_t nc = (n_rows - t0) < L.chunk ? (n_rows - t0) : L.chunk;
+  const int64_t H = hidden_size, V = vocab_local;
+  const auto* X = static_cast<const uint16_t*>(hidden);
+  auto* pt = reinterpret_cast<uint16_t*>(ws + L.off_pt);
+  auto* dz = reinterpret_cast<uint16_t*>(ws + L.off_dz);
+  auto* xt = reinterpret_cast<uint16_t*>(ws + L.off_xt);
+  const auto* wt = reinterpret_cast<const uint16_t*>(ws + L.off_wt);
+  const float* pmax = reinterpret_cast<const float*>(ws + L.off_part);
+  // dZ of the chunk, vocabulary-major in place of P^T and token-major into dz.
+  hipLaunchKernelGGL(lmhead_dz_rescale_kernel,
+                     dim3(static_cast<unsigned>(L.vpad / kRsRows),
+                          static_cast<unsigned>(L.ldt / kRsToks)),
+                     dim3(256), 0, s, pt, L.ldt, dz, L.vpad, V, nc, pmax, L.nb, g_max + t0,
+                     g_sumexp_m1 + t0, target_logit + t0, target + t0, vocab_start,
+                     grad_output + t0 * gout_stride, gout_stride, gout_div);
+  if ((st = launch_status())) return st;
+  // X_c^T [H, ldt], zero beyond the chunk's tokens: the dW GEMM's B operand.
+  if ((st = launch_transpose(X + t0 * H, nc, H, H, xt, L.ldt, s))) return st;
+  // dX rows of the chunk = dZ_c W (K = the padded vocabulary; the padding of
+  // dz and W^T is zero).
+  if ((st = launch_gemm_store(0, dz, L.vpad, nc, wt, L.vpad, H, L.vpad,
+                              static_cast<uint16_t*>(grad_hidden) + t0 * H, nullptr, H, s)))
+    return st;
+  // dW (+)= dZ_c^T X_c (K = the chunk's padded tokens), accumulated in fp32
+  // across chunks and rounded to bf16 by the last.
+  int mode;
+  if (L.n_chunks == 1) mode = 0;
+  else if (chunk_index == 0) mode = 1;
+  else if (chunk_index + 1 < L.n_chunks) mode = 2;
+  else mode = 3;
+  return launch_gemm_store(mode, pt, L.ldt, V, xt, L.ldt, H, L.ldt,
+                           static_cast<uint16_t*>(grad_weight),
+                           reinterpret_cast<float*>(ws + L.off_acc), H, s);
 }
 
 }  // extern "C"

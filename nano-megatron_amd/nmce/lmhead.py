@@ -12,24 +12,40 @@ becomes
 with ``x`` the (already TP-mapped, model.py:188-191) hidden state and ``W`` the
 LM head's vocabulary shard ``[V/tp, H]``. The loss and its gradients with
 respect to ``x`` and ``W`` are those of the two-step reference, but the
-``[tokens, V/tp]`` logits are never stored: the forward keeps two floats per
-token and the backward recomputes the logits one vocabulary chunk at a time.
+``[tokens, V/tp]`` logits are never stored.
+
+When a gradient is wanted (grad mode on, ``x`` or ``W`` requiring grad) the
+wrapper takes the one-pass path: the forward goes through the tokens in
+chunks, keeps each chunk's exponentials, forms dZ once the chunk's row
+statistics are combined, and computes dX and dW right away for the upstream
+value that the last backward from the same call site received (1.0 at
+first), as the reference's forward computes the softmax that its backward
+returns (cross_entropy.py:48-49). The logits are computed once (6 N V H flops
+in all). The backward hands the gradients out, rescaled when its upstream
+value differs. Otherwise (no gradient wanted, ``one_pass=False``, or the
+per-token Function) the forward keeps two floats per token and the backward
+recomputes the logits one vocabulary chunk at a time.
 
 Numerics: the reference runs the projection in bf16 under autocast
 (model.py:255-257), so its logits are rounded to bf16 before the loss; here
 they stay fp32 from the MFMA accumulators into the softmax. The logit
 gradient is rounded to bf16 before the two backward products, as the
-reference's autocast matmul backward consumes a bf16 gradient.
+reference's autocast matmul backward consumes a bf16 gradient; on the
+one-pass path it is formed from the kept exponentials, themselves bf16, so
+it carries two roundings (each relative 2^-9) instead of one.
 
 Both ``x`` and ``W`` must be bf16 on a ROCm device; there is no CPU path.
 """
 
 from __future__ import annotations
 
+import sys
+
 import torch
 
 from . import _lib
-from .cross_entropy import _check_target, _exchange_stats, _launch, launch_target_check
+from .cross_entropy import (_check_hint, _check_target, _exchange_stats, _launch, _site_hint,
+                            launch_target_check)
 from .mappings import (
     copy_to_tensor_parallel_region,
     gather_from_sequence_parallel_region,
@@ -53,7 +69,12 @@ DEFAULT_VOCAB_CHUNK = 32768
 # (nmce_lmhead_ce_bwd, everything in one C call). The fused parts -- the
 # forward statistics GEMM and the recomputation of dZ -- are libnmce kernels
 # either way.
-BACKWARD_GEMM = "library"
+BACKWARD_GEMM = "nmce"
+
+# Tokens per chunk of the one-pass path: each chunk holds its exponentials and
+# its dZ in both layouts, 4 * chunk * V bytes (bf16), so no tensor the size of
+# the full logits exists; with more than one chunk dW is accumulated in fp32.
+DEFAULT_TOKEN_CHUNK = 8192
 
 _ALIGN = 64  # hidden size granularity of the GEMM kernels
 
@@ -140,6 +161,164 @@ def _backward_library_gemm(lib, x, w, tgt, vocab_start, row_stat, go, gstride, v
     return acc.to(torch.bfloat16)
 
 
+def _fused_layout(lib, n: int, hp: int, v: int, token_chunk: int) -> dict:
+    import ctypes
+    buf = (ctypes.c_int64 * _lib.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
+    _lib.check(lib.nmce_lmhead_ce_fused_layout(n, hp, v, token_chunk, ctypes.addressof(buf)),
+               "nmce_lmhead_ce_fused_layout")
+    keys = ("total", "chunk", "n_chunks", "ldt", "vpad", "nb", "off_wt", "off_xt", "off_pt",
+            "off_dz", "off_part", "off_acc")
+    return dict(zip(keys, (int(b) for b in buf)))
+
+
+def _check_fused_operands(hidden, weight, vocab_start, vocab_end):
+    if not (hidden.is_cuda and weight.is_cuda):
+        raise RuntimeError("nmce: hidden and weight must be on a ROCm device "
+                           "(there is no CPU path)")
+    if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+        raise TypeError("nmce: the fused LM head computes in bf16; got hidden "
+                        f"{hidden.dtype}, weight {weight.dtype}")
+    if weight.dim() != 2 or hidden.shape[-1] != weight.shape[1]:
+        raise ValueError(f"nmce: hidden {tuple(hidden.shape)} and weight "
+                         f"{tuple(weight.shape)} do not share the hidden size")
+    if weight.shape[0] != vocab_end - vocab_start:
+        raise ValueError(f"nmce: weight holds {weight.shape[0]} vocabulary rows but the "
+                         f"shard [{vocab_start}, {vocab_end}) has {vocab_end - vocab_start}")
+
+
+class _LMHeadVocabParallelCrossEntropyMean(torch.autograd.Function):
+    """Mean loss of ``hidden @ weight.t()`` over a vocabulary shard, one pass.
+
+    ``forward(hidden, weight, target, vocab_start, vocab_end, group,
+    world_size, hint, token_chunk)`` returns the 0-dim mean of the per-token
+    loss (torch's mean, cross_entropy.py:85) and computes the gradients of
+    ``hidden`` and ``weight`` for the upstream value ``usable(hint[0])`` of
+    the mean, chunk by chunk over the tokens (nmce_lmhead_ce_fused_*). The
+    backward hands them out when its upstream value is that one and rescales
+    them otherwise (within two bf16 units in the last place; exactly for a
+    power-of-two ratio), writing the value it received into ``hint``. A
+    second backward through the same graph recomputes them (the vocabulary-
+    chunked backward of ``_LMHeadVocabParallelCrossEntropy``).
+    """
+
+    @staticmethod
+    def forward(ctx, hidden, weight, target, vocab_start, vocab_end, group, world_size, hint,
+                token_chunk=None):
+        _check_fused_operands(hidden, weight, vocab_start, vocab_end)
+        _check_target(target, hidden.shape[:-1], hidden.device)
+        lib = _lib.load()
+        dev = hidden.device
+        stream = _lib.stream_handle(dev)
+        H = hidden.shape[-1]
+        V = weight.shape[0]
+        hp = (H + _ALIGN - 1) // _ALIGN * _ALIGN
+        x = _padded_hidden(hidden.reshape(-1, H), hp)
+        w = _padded_hidden(weight, hp)
+        n = x.shape[0]
+        tgt = target.reshape(-1)
+        if not tgt.is_contiguous():
+            tgt = tgt.contiguous()
+        ctx.vocab_start = vocab_start
+        ctx.hidden_shape = hidden.shape
+        ctx.H = H
+        ctx.hint = hint
+        ctx.handed_out = False
+        if n == 0:  # an empty batch: nothing to launch; torch's mean of nothing
+            ctx.empty = True
+            ctx.weight_shape = weight.shape
+            return torch.empty(0, dtype=torch.float32, device=dev).mean()
+        ctx.empty = False
+        chunk = DEFAULT_TOKEN_CHUNK if token_chunk is None else int(token_chunk)
+        L = _fused_layout(lib, n, hp, V, chunk)
+        ws = _workspace(L["total"], dev)
+        args = (x.data_ptr(), w.data_ptr(), _lib.NMCE_BF16, n, hp, V)
+        assumed = torch.empty(1, dtype=torch.float32, device=dev)
+        _launch("nmce_hint_assume", lib.nmce_hint_assume, hint.data_ptr(), assumed.data_ptr(),
+                stream)
+        _launch("nmce_lmhead_ce_fused_prepare", lib.nmce_lmhead_ce_fused_prepare, *args, chunk,
+                ws.data_ptr(), ws.numel(), stream)
+        local = torch.empty((3, n), dtype=torch.float32, device=dev)  # max, sum - 1, target z
+        out = torch.empty((3, n), dtype=torch.float32, device=dev)    # loss, max, sum - 1
+        dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
+        dw = torch.empty((V, hp), dtype=torch.bfloat16, device=dev)
+        step = L["chunk"]
+        for c in range(L["n_chunks"]):
+            t0 = c * step
+            nc = min(step, n - t0)
+            _launch("nmce_lmhead_ce_fused_chunk_stats", lib.nmce_lmhead_ce_fused_chunk_stats,
+                    *args, tgt.data_ptr(), vocab_start, chunk, c, local[0].data_ptr(),
+                    local[1].data_ptr(), local[2].data_ptr(), ws.data_ptr(), ws.numel(), stream)
+            if world_size == 1:
+                base, stride = local.data_ptr() + 4 * t0, 3 * n
+            else:
+                stats = _exchange_stats(local[:, t0:t0 + nc], group, world_size)
+                base, stride = stats.data_ptr(), 3 * nc
+            _launch("nmce_ce_combine", lib.nmce_ce_combine, base, base + 4 * (stride // 3),
+                    base + 8 * (stride // 3), world_size, stride, nc,
+                    out[0].data_ptr() + 4 * t0, out[1].data_ptr() + 4 * t0,
+                    out[2].data_ptr() + 4 * t0, stream)
+            _launch("nmce_lmhead_ce_fused_chunk_grads", lib.nmce_lmhead_ce_fused_chunk_grads,
+                    *args, tgt.data_ptr(), vocab_start, chunk, c, out[1].data_ptr(),
+                    out[2].data_ptr(), local[2].data_ptr(), assumed.data_ptr(), 0, float(n),
+                    dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), ws.numel(), stream)
+        ctx.save_for_backward(x, w, tgt, out[1:], dx, dw, assumed)
+        return out[0].mean()
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        if ctx.empty:
+            dev = grad_output.device
+            return (torch.zeros(ctx.hidden_shape, dtype=torch.bfloat16, device=dev),
+                    torch.zeros(ctx.weight_shape, dtype=torch.bfloat16, device=dev),
+                    None, None, None, None, None, None, None)
+        x, w, tgt, row_stat, dx, dw, assumed = ctx.saved_tensors
+        lib = _lib.load()
+        go = grad_output.reshape(1)
+        if go.dtype != torch.float32:
+            go = go.float()
+        n, hp = x.shape
+        V = w.shape[0]
+        if ctx.handed_out:
+            # dx / dw belong to the first backward's consumers: recompute.
+            g_tok = go / n  # the per-token value MeanBackward forms, broadcast
+            dw = torch.empty((V, hp), dtype=torch.bfloat16, device=x.device)
+            dx = _recompute_backward(lib, x, w, tgt, ctx.vocab_start, row_stat, g_tok, 0,
+                                     DEFAULT_VOCAB_CHUNK, dw)
+        else:
+            stream = _lib.stream_handle(x.device)
+            _launch("nmce_ce_grad_rescale_unless", lib.nmce_ce_grad_rescale_unless,
+                    dx.data_ptr(), _lib.NMCE_BF16, n, hp, hp, go.data_ptr(), assumed.data_ptr(),
+                    ctx.hint.data_ptr(), stream)
+            _launch("nmce_ce_grad_rescale_unless", lib.nmce_ce_grad_rescale_unless,
+                    dw.data_ptr(), _lib.NMCE_BF16, V, hp, hp, go.data_ptr(), assumed.data_ptr(),
+                    None, stream)
+            ctx.handed_out = True
+        H = ctx.H
+        if hp != H:
+            dx = dx[:, :H]
+            dw = dw[:, :H].contiguous()
+        return (dx.reshape(ctx.hidden_shape), dw, None, None, None, None, None, None, None)
+
+
+def _recompute_backward(lib, x, w, tgt, vocab_start, row_stat, go, gstride, vocab_chunk, dw):
+    """dX (returned) and dW (into ``dw``) by recomputing the logits one
+    vocabulary chunk at a time, on the route BACKWARD_GEMM names."""
+    n, hp = x.shape
+    V = w.shape[0]
+    dev = x.device
+    if BACKWARD_GEMM == "nmce":
+        dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
+        ws = _workspace(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, hp, V, vocab_chunk), dev)
+        _launch("nmce_lmhead_ce_bwd", lib.nmce_lmhead_ce_bwd, x.data_ptr(), w.data_ptr(),
+                _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), vocab_start,
+                row_stat[0].data_ptr(), row_stat[1].data_ptr(), go.data_ptr(), gstride,
+                dx.data_ptr(), dw.data_ptr(), vocab_chunk, ws.data_ptr(), ws.numel(),
+                _lib.stream_handle(dev))
+        return dx
+    return _backward_library_gemm(lib, x, w, tgt, vocab_start, row_stat, go, gstride,
+                                  vocab_chunk, dw)
+
+
 class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
     """Per-token loss of ``hidden @ weight.t()`` over a vocabulary shard.
 
@@ -154,18 +333,7 @@ class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
     @staticmethod
     def forward(ctx, hidden, weight, target, vocab_start, vocab_end, group, world_size,
                 vocab_chunk=None):
-        if not (hidden.is_cuda and weight.is_cuda):
-            raise RuntimeError("nmce: hidden and weight must be on a ROCm device "
-                               "(there is no CPU path)")
-        if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
-            raise TypeError("nmce: the fused LM head computes in bf16; got hidden "
-                            f"{hidden.dtype}, weight {weight.dtype}")
-        if weight.dim() != 2 or hidden.shape[-1] != weight.shape[1]:
-            raise ValueError(f"nmce: hidden {tuple(hidden.shape)} and weight "
-                             f"{tuple(weight.shape)} do not share the hidden size")
-        if weight.shape[0] != vocab_end - vocab_start:
-            raise ValueError(f"nmce: weight holds {weight.shape[0]} vocabulary rows but the "
-                             f"shard [{vocab_start}, {vocab_end}) has {vocab_end - vocab_start}")
+        _check_fused_operands(hidden, weight, vocab_start, vocab_end)
         _check_target(target, hidden.shape[:-1], hidden.device)
         lib = _lib.load()
         dev = hidden.device
@@ -232,18 +400,8 @@ class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
                 go = go.contiguous()
             gstride = 1
         dw = torch.empty((V, hp), dtype=torch.bfloat16, device=dev)
-        if BACKWARD_GEMM == "nmce":
-            dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
-            ws = _workspace(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, hp, V, ctx.vocab_chunk),
-                            dev)
-            _launch("nmce_lmhead_ce_bwd", lib.nmce_lmhead_ce_bwd, x.data_ptr(), w.data_ptr(),
-                    _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), ctx.vocab_start,
-                    row_stat[0].data_ptr(), row_stat[1].data_ptr(), go.data_ptr(), gstride,
-                    dx.data_ptr(), dw.data_ptr(), ctx.vocab_chunk, ws.data_ptr(), ws.numel(),
-                    _lib.stream_handle(dev))
-        else:
-            dx = _backward_library_gemm(lib, x, w, tgt, ctx.vocab_start, row_stat, go, gstride,
-                                        ctx.vocab_chunk, dw)
+        dx = _recompute_backward(lib, x, w, tgt, ctx.vocab_start, row_stat, go, gstride,
+                                 ctx.vocab_chunk, dw)
         H = ctx.H
         if hp != H:
             dx = dx[:, :H]
@@ -260,7 +418,10 @@ def lmhead_vocab_parallel_cross_entropy(
     ctx,
     *,
     vocab_chunk: int | None = None,
+    token_chunk: int | None = None,
     validate: bool = True,
+    one_pass: bool = True,
+    upstream_hint: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Mean cross-entropy of ``hidden @ weight.t()`` against ``target``.
 
@@ -269,6 +430,14 @@ def lmhead_vocab_parallel_cross_entropy(
     model.py:192) without storing the logits. ``hidden`` is ``[b, s, H]`` (or
     ``[tokens, H]``), ``weight`` is ``[V/tp, H]``; returns a 0-dim fp32
     tensor. Same ``ValueError`` as the reference for an out-of-range target.
+
+    When a gradient is wanted the forward is one pass (module docstring),
+    going through ``token_chunk`` tokens at a time (default
+    ``DEFAULT_TOKEN_CHUNK``) and assuming the upstream value held by
+    ``upstream_hint`` (a one-element fp32 device tensor; default: one per
+    call site). ``one_pass=False`` selects the forward that keeps only the
+    row statistics, with a backward that recomputes the logits in chunks of
+    ``vocab_chunk`` vocabulary rows.
 
     The product is computed in bf16. Inside a bf16 autocast region (as
     model.py:255-257 runs the LM head) an fp32 ``hidden`` or ``weight`` is cast
@@ -291,12 +460,25 @@ def lmhead_vocab_parallel_cross_entropy(
         weight = weight.to(torch.bfloat16)
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
     _check_target(target, hidden.shape[:-1], hidden.device)
+    want_grad = torch.is_grad_enabled() and (hidden.requires_grad or weight.requires_grad)
     pending = launch_target_check(target, vocab_size) if validate else None
-    loss = _LMHeadVocabParallelCrossEntropy.apply(
-        hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, vocab_chunk)
+    if one_pass and want_grad:
+        if upstream_hint is None:
+            caller = sys._getframe(1)
+            hint = _site_hint(hidden.device, (caller.f_code.co_filename, caller.f_lineno))
+        else:
+            _check_hint(upstream_hint, hidden.device)
+            hint = upstream_hint
+        loss = _LMHeadVocabParallelCrossEntropyMean.apply(
+            hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, hint,
+            token_chunk)
+    else:
+        loss = _LMHeadVocabParallelCrossEntropy.apply(
+            hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size,
+            vocab_chunk).mean()
     if pending is not None:
         pending.raise_if_bad()
-    return loss.mean()
+    return loss
 
 
 class FusedParallelLMHead(torch.nn.Module):
@@ -328,6 +510,10 @@ class FusedParallelLMHead(torch.nn.Module):
         self.weight.tensor_parallel_sharded = True
         self.sequence_parallel = bool(getattr(config, "sequence_parallel", False))
         self.vocab_chunk = None  # backward chunk; None = DEFAULT_VOCAB_CHUNK
+        self.token_chunk = None  # one-pass chunk; None = DEFAULT_TOKEN_CHUNK
+        # The upstream value the one-pass forward assumes, per module and
+        # device (created on first use on that device).
+        self._hints: dict = {}
         torch.nn.init.normal_(self.weight, std=0.02)
 
     def vocab_range(self) -> tuple[int, int]:
@@ -349,5 +535,12 @@ class FusedParallelLMHead(torch.nn.Module):
         else:
             rows = copy_to_tensor_parallel_region(x, self.ctx)
             target = labels
+        dev = rows.device
+        hint = self._hints.get(dev)
+        if hint is None:
+            hint = torch.ones(1, dtype=torch.float32, device=dev)
+            self._hints[dev] = hint
         return lmhead_vocab_parallel_cross_entropy(rows, self.weight, target, start, end,
-                                                   self.ctx, vocab_chunk=self.vocab_chunk)
+                                                   self.ctx, vocab_chunk=self.vocab_chunk,
+                                                   token_chunk=self.token_chunk,
+                                                   upstream_hint=hint)

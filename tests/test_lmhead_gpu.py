@@ -360,8 +360,9 @@ def test_fused_two_shards_combined(v, chunk):
 @pytest.mark.parametrize("route", ["library", "nmce"])
 @pytest.mark.parametrize("chunk", [256, 768, None])
 def test_dropin_backward_routes(route, chunk):
-    """The drop-in backward through either GEMM route (library GEMMs on the
-    prepared buffers, or libnmce's own) against the fp64 closed form."""
+    """The drop-in's recomputing backward (one_pass=False) through either GEMM
+    route (library GEMMs on the prepared buffers, or libnmce's own) against
+    the fp64 closed form."""
     import nmce
     import nmce.lmhead as LH
     n, h, v = 320, 128, 1900
@@ -373,7 +374,7 @@ def test_dropin_backward_routes(route, chunk):
         wd = w.to(DEV).requires_grad_(True)
         loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v,
                                                         nmce.ParallelContext.single(),
-                                                        vocab_chunk=chunk)
+                                                        vocab_chunk=chunk, one_pass=False)
         loss.backward()
     finally:
         LH.BACKWARD_GEMM = saved
@@ -613,15 +614,17 @@ def _lse_all(xd, wd, chunk=1024):
     return torch.cat(out)
 
 
-@pytest.mark.parametrize("route", ["library", "nmce"])
+@pytest.mark.parametrize("route", ["one_pass", "library", "nmce"])
 @pytest.mark.parametrize("cfg", ["c4", "c5"])
 def test_fused_workload(cfg, route, monkeypatch):
     """c4: hidden [16384, 4096] ~ N(0,1), W [128256, 4096] ~ N(0, 0.02^2), uniform
     targets. c5: hidden [16384, 3072], W [256000, 3072] ~ N(0, 0.05^2) with 64
-    rows x30, Zipf(1.1) targets (logits far beyond +-60). Both backward
-    routes: the library's products, and the hand-written one with dX
-    accumulated in fp32 over the 32768-row vocabulary chunks (4 at c4, 8 at
-    c5)."""
+    rows x30, Zipf(1.1) targets (logits far beyond +-60). Every route: the
+    drop-in's default one-pass path (two chunks of 8192 tokens, dW
+    accumulated in fp32 across them; the mean loss equal to the per-token
+    Function's, bit for bit), and the recomputing backward through the
+    library's products or the hand-written one (dX accumulated in fp32 over
+    the 32768-row vocabulary chunks, 4 at c4, 8 at c5)."""
     import nmce
     from nmce import lmhead as lm
     monkeypatch.setattr(lm, "BACKWARD_GEMM", route)
@@ -645,9 +648,18 @@ def test_fused_workload(cfg, route, monkeypatch):
     ctx = nmce.ParallelContext.single()
     xd = x.clone().requires_grad_(True)
     wd = w.clone().requires_grad_(True)
-    per_tok = nmce._LMHeadVocabParallelCrossEntropy.apply(xd, wd, t, 0, v, None, 1, None)
-    loss = per_tok.mean()
-    loss.backward()
+    if route == "one_pass":
+        hint = torch.ones(1, dtype=torch.float32, device=DEV)
+        loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t, 0, v, ctx,
+                                                        upstream_hint=hint)
+        loss.backward()
+        with torch.no_grad():
+            per_tok = nmce._LMHeadVocabParallelCrossEntropy.apply(x, w, t, 0, v, None, 1, None)
+        assert loss.item() == per_tok.mean().item()
+    else:
+        per_tok = nmce._LMHeadVocabParallelCrossEntropy.apply(xd, wd, t, 0, v, None, 1, None)
+        loss = per_tok.mean()
+        loss.backward()
     torch.cuda.synchronize()
     gval = 1.0 / n
     rows = torch.randperm(n, device=DEV, generator=g)[:256]
@@ -673,6 +685,89 @@ def test_fused_workload(cfg, route, monkeypatch):
             zmax = max(zmax, (x[i:i + 2048].float() @ w[hot].float().t()).abs().max().item())
         print(f"[fused-workload] c5 max |logit| on the scaled rows: {zmax:.1f}", flush=True)
         assert zmax > 60.0
+
+
+# ---------------------------------------------------------------------------
+# The one-pass path (the drop-in's default when a gradient is wanted)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("n,h,v,chunk", [(300, 128, 777, None), (1000, 192, 1900, 256),
+                                         (513, 100, 3001, 256), (64, 64, 1, None),
+                                         (700, 64, 129, 512), (2048, 256, 20000, 768)])
+def test_one_pass_fused_against_oracle(n, h, v, chunk):
+    """The drop-in's one-pass forward (dX and dW formed chunk by chunk over the
+    tokens, for the assumed upstream 1.0) against the fp64 closed form: one
+    chunk, several with a short last one, a hidden size padded to 64, a
+    vocabulary of one row and one that ends a row into a 128-row block."""
+    import nmce
+    print(f"[gpu] one-pass fused n={n} h={h} v={v} chunk={chunk}", flush=True)
+    x, w, t = make_inputs(n, h, v, seed=n + v, w_std=0.5)
+    xd = x.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    hint = torch.ones(1, dtype=torch.float32, device=DEV)
+    loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v,
+                                                    nmce.ParallelContext.single(),
+                                                    token_chunk=chunk, upstream_hint=hint)
+    loss.backward()
+    rl, _, rdx, rdw = fp64_reference(x, w, t)
+    assert abs(loss.item() - rl.mean()) <= 1e-5 * abs(rl.mean()) + 1e-30
+    check_grad(xd.grad.float().cpu().numpy(), rdx, "dH")
+    check_grad(wd.grad.float().cpu().numpy(), rdw, "dW")
+
+
+def test_one_pass_fused_follows_the_upstream_value():
+    """A loss scaled by 0.25 each step: the first backward rescales the forward's
+    gradients (a power-of-two ratio, so exactly) and records 0.25, after which
+    the forward's gradients stand; 0.37 rescales by a ratio that rounds. Every
+    step against the fp64 closed form for its upstream value."""
+    import nmce
+    n, h, v = 512, 128, 1500
+    x, w, t = make_inputs(n, h, v, seed=61, w_std=0.5)
+    hint = torch.ones(1, dtype=torch.float32, device=DEV)
+    grads = []
+    for scale in (0.25, 0.25, 0.37):
+        xd = x.to(DEV).requires_grad_(True)
+        wd = w.to(DEV).requires_grad_(True)
+        loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v,
+                                                        nmce.ParallelContext.single(),
+                                                        token_chunk=256, upstream_hint=hint)
+        (loss * scale).backward()
+        assert hint.item() == np.float32(scale)
+        rl, _, rdx, rdw = fp64_reference(x, w, t, g=np.full(n, scale / n))
+        check_grad(xd.grad.float().cpu().numpy(), rdx, f"dH at {scale}")
+        check_grad(wd.grad.float().cpu().numpy(), rdw, f"dW at {scale}")
+        grads.append((xd.grad.clone(), wd.grad.clone()))
+    # the hit (second step) and the exact power-of-two rescale agree bit for bit
+    assert torch.equal(grads[0][0].view(torch.int16), grads[1][0].view(torch.int16))
+    assert torch.equal(grads[0][1].view(torch.int16), grads[1][1].view(torch.int16))
+
+
+def test_one_pass_fused_retain_graph_and_no_grad():
+    """A second backward through the same graph recomputes the gradients (the
+    first ones were handed out), so the leaves accumulate both; a forward
+    under no_grad computes no gradient and returns the same loss."""
+    import nmce
+    n, h, v = 384, 128, 1200
+    x, w, t = make_inputs(n, h, v, seed=67, w_std=0.5)
+    ctx = nmce.ParallelContext.single()
+    xd = x.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v, ctx,
+                                                    token_chunk=256)
+    loss.backward(retain_graph=True)
+    (loss * 0.5).backward()
+    rl, _, rdx, rdw = fp64_reference(x, w, t, g=np.full(n, 1.5 / n))
+    check_grad(xd.grad.float().cpu().numpy(), rdx, "dH, two backwards")
+    check_grad(wd.grad.float().cpu().numpy(), rdw, "dW, two backwards")
+    with torch.no_grad():
+        torch.cuda.synchronize()
+        before = torch.cuda.memory_allocated()
+        torch.cuda.reset_peak_memory_stats()
+        nograd = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v, ctx)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated() - before
+    assert nograd.item() == loss.item()
+    assert peak < n * v * 2, f"a no-grad forward allocated {peak} bytes"
 
 
 def test_fused_empty_batch():
