@@ -23,6 +23,8 @@ Workloads:
                 the peer rank's statistics are computed once up front and
                 handed over by an emulated all-gather, the combine is local
   c1            fp32 [4,256,32000] ~ N(0,2^2) (the reference's CPU config)
+  wide          TP=1, bf16 [4,2048,128256] ~ N(0,1): a whole vocabulary of
+                128256 entries through the one-pass path (rows held partly in LDS)
   c4            fused: hidden bf16 [16384,4096] ~ N(0,1), tied weight bf16
                 [128256,4096] ~ N(0,0.02^2), targets U[0,128256)
   c5            fused stress: hidden [16384,3072], weight [256000,3072] ~
@@ -36,7 +38,8 @@ statistics GEMM (2 x tokens x vocab x hidden), over its average launch time
 measured with HIP events on the launch stream during the timed steps.
 Without ``--workload`` the line is c2 (the default path: one read of the
 logits, gradient in place) with nested objects ``two_pass`` (c2 on the
-two-pass path), ``c3``, ``c1``, ``fused`` (c4) and ``c5``, each with its own
+two-pass path), ``c3``, ``c1``, ``wide`` (c2's path at a 128256-entry
+vocabulary), ``fused`` (c4) and ``c5``, each with its own
 ``roofline``, ``kernels_ms`` and ``cpu_baseline``. ``cpu_baseline`` is the
 torch-CPU restatement of the reference's op sequence (oracle/ce_restate.py)
 timed on this host on a bounded sample of the same workload (repeated for
@@ -69,6 +72,9 @@ WORKLOADS = {
                b=4, s=4096, v=64128, tp=2, rank=1, sigma=1.5, dtype="bf16"),
     "c1": dict(desc="fp32 logits [4,256,32000] ~ N(0,2^2), targets U[0,32000), TP=1",
                b=4, s=256, v=32000, tp=1, rank=0, sigma=2.0, dtype="f32"),
+    "wide": dict(desc="unfused TP=1, bf16 logits [4,2048,128256] ~ N(0,1), targets "
+                      "U[0,128256) (a whole 128256-entry vocabulary on one GPU)",
+                 b=4, s=2048, v=128256, tp=1, rank=0, sigma=1.0, dtype="bf16"),
     "c4": dict(desc="fused LM head + CE: hidden bf16 [16384,4096] ~ N(0,1), tied weight bf16 "
                     "[128256,4096] ~ N(0,0.02^2), targets U[0,128256)",
                fused=True, n=16384, h=4096, v=128256, w_std=0.02, hot_rows=0, zipf=None),
@@ -80,7 +86,7 @@ WORKLOADS = {
 # Nested objects of the default line: (key, workload, one_pass). The unfused
 # ones take --steps/--warmup, the fused ones --fused-steps/--fused-warmup.
 NESTED = [("two_pass", "c2", False), ("c3", "c3", True), ("c1", "c1", True),
-          ("fused", "c4", True), ("c5", "c5", True)]
+          ("wide", "wide", True), ("fused", "c4", True), ("c5", "c5", True)]
 
 
 def parse_args():

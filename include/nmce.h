@@ -205,7 +205,7 @@ int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, i
  * entry of `grad` is multiplied by grad_output[0] / assumed[0] in fp32 and
  * rounded back to the gradient's dtype (cross_entropy.py:64: the gradient is
  * linear in grad_output). The logits are gone, so this cannot recompute; the
- * result is within two units in the last place of the gradient dtype of the
+ * result is within four (fp32) or two (bf16) units in the last place of the
  * recomputed one, and equal to it when the ratio is a power of two.
  * grad_output[0] also goes to `observed` (may be NULL), the next forward's
  * grad_expected. Same layout requirements as nmce_ce_fwd_bwd.

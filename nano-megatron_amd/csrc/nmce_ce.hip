@@ -517,6 +517,176 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
   }
 }
 
+// Rows wider than 8 vectors per lane (up to 16): ce_fwdbwd_kernel with the
+// lane's vectors 0..6 in registers and 7..15 in LDS (144 KiB, one 1024-lane
+// workgroup per compute unit; 128 registers per lane hold the current and
+// next row's register part and the arithmetic without spilling). Direct-to-LDS loads fill the LDS part; the
+// next row's LDS part is loaded as soon as this row's LDS part has been read
+// for its gradient, while the register part's gradient is written, and the
+// next row's register part is loaded right after this row's fold. Same fold
+// order, merges and per-element arithmetic as ce_fwdbwd_kernel (and so as
+// ce_stats_kernel and ce_bwd_flat_kernel): bit-identical outputs.
+// Cache-policy word of the buffer loads and stores: nt (streaming).
+constexpr int kBufNonTemporal = 2;
+constexpr int kWideLo = 7;
+constexpr int kWideHi = 9;
+constexpr int kWideLdsBytes = kWideHi * kStatsBlock * 16;  // 144 KiB
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <typename T>
+__global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
+    const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
+    const int64_t* __restrict__ target, float* __restrict__ loss, float* __restrict__ out_max,
+    float* __restrict__ out_sum1, const float* __restrict__ expect_in,
+    float* __restrict__ assumed, float gdiv) {
+  using E = Elem<T>;
+  constexpr int EPV = E::kPerVec;
+  constexpr int kBlock = kStatsBlock;
+  constexpr int kWaves = kBlock / 64;
+  constexpr bool kExact = sizeof(T) == 4;
+  extern __shared__ __align__(16) char lds_dyn[];
+  u32x4* hi = reinterpret_cast<u32x4*>(lds_dyn);  // vector kWideLo + k of lane t: hi[k * kBlock + t]
+  const float expect = usable_hint(expect_in[0]);
+  if (blockIdx.x == 0 && threadIdx.x == 0) assumed[0] = expect;
+  __shared__ float sm_m[kWaves];
+  __shared__ float sm_s[kWaves];
+  __shared__ float sm_row[3];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int64_t nvec = V / EPV;
+  // Vectors tid, tid + kBlock, ... of a row that exist: cnt of them (<= 16).
+  const int cnt = nvec > tid ? static_cast<int>((nvec - tid + kBlock - 1) / kBlock) : 0;
+  const float go = expect / gdiv;
+  u32x4 cur[kWideLo], nxt[kWideLo];
+  // Rows are addressed through buffer resources on the row: one per-lane
+  // offset (tid * 16) serves every vector and the vector's place goes in the
+  // scalar offset. The range check covers the per-lane offset only, so every
+  // access is guarded by the lane's vector count instead.
+  const uint32_t row_bytes = static_cast<uint32_t>(nvec * 16);
+  auto row_rsrc = [&](const void* base) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0,
+                                             static_cast<int>(row_bytes), 0x00020000);
+  };
+  const uint32_t voff = static_cast<uint32_t>(tid) * 16u;
+  auto load_lo = [&](int64_t r, u32x4* v) {
+    const auto rs = row_rsrc(x + r * ld);
+#pragma unroll
+    for (int k = 0; k < kWideLo; ++k)
+      if (k < cnt)
+        v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff, k * kBlock * 16, kBufNonTemporal);
+  };
+  // Row r's vectors kWideLo.. into LDS: the 64 lanes of wave w fill the 1 KiB
+  // at hi[k * kBlock + 64 w], lane l its 16 bytes at + l. The buffer resource
+  // spans the row exactly (offsets past it would read 0, and none is issued).
+  auto load_hi = [&](int64_t r) {
+    const uint64_t addr = reinterpret_cast<uint64_t>(x + r * ld);
+    i32x4_t rsrc;
+    rsrc[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(addr & 0xffffffffu));
+    rsrc[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(addr >> 32));
+    rsrc[2] = static_cast<int>(nvec * 16);
+    rsrc[3] = 0x00020000;
+#pragma unroll
+    for (int k = 0; k < kWideHi; ++k)
+      if (kWideLo + k < cnt)
+        raw_buffer_load_lds(rsrc, (lds_void_t*)(hi + k * kBlock + wave * 64), 16,
+                            static_cast<int>(voff) + (kWideLo + k) * kBlock * 16, 0, 0, 0);
+  };
+  int64_t row = blockIdx.x;
+  if (row < n_rows) {
+    load_lo(row, cur);
+    load_hi(row);
+  }
+  for (; row < n_rows; row += gridDim.x) {
+    const T* xr = x + row * ld;
+    // ce_stats_kernel's order: vectors k and k + 1 (kBlock apart) together
+    // while both exist, then the one left, if any. Vectors below kWideLo
+    // come from registers, the rest from LDS once every wave's loads of this
+    // row have landed (the pair that straddles waits for them too).
+    auto vec = [&](int k) -> u32x4 {
+      return k < kWideLo ? cur[k] : hi[(k - kWideLo) * kBlock + tid];
+    };
+    float m = kMaxFloor, a = kExact ? -1.0f : 0.0f;
+    bool paired = true;
+#pragma unroll
+    for (int k = 0; k < kWideLo + kWideHi; k += 2) {
+      if (k + 2 > kWideLo && k <= kWideLo) {  // the first pair that reads LDS
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+      }
+      if (paired && k + 1 < cnt) {
+        float f[2 * EPV];
+        E::unpack(vec(k), f);
+        E::unpack(vec(k + 1), f + EPV);
+        lane_fold<kExact, 2 * EPV>(m, a, f);
+      } else {
+        paired = false;
+        if (k < cnt) {
+          float f[EPV];
+          E::unpack(vec(k), f);
+          lane_fold<kExact, EPV>(m, a, f);
+        }
+      }
+    }
+    const int64_t next = row + gridDim.x;
+    if (next < n_rows) load_lo(next, nxt);
+    float t = kExact ? a : a - 1.0f;
+    wave_merge_excess(m, t);
+    if (lane == 0) {
+      sm_m[wave] = m;
+      sm_s[wave] = t;
+    }
+    __syncthreads();
+    if (wave == 0) {
+      float M = lane < kWaves ? sm_m[lane] : kMaxFloor;
+      float T1 = lane < kWaves ? sm_s[lane] : -1.0f;
+      wave_merge_excess(M, T1);
+      if (lane == 0) {
+        // A target outside [0, V) picks nothing, as in ce_stats_kernel.
+        const int64_t lt = target[row];
+        const float xt = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
+        out_max[row] = M;
+        out_sum1[row] = T1;
+        loss[row] = log1pf(T1) - (xt - M);
+        sm_row[0] = M;
+        sm_row[1] = T1;
+        sm_row[2] = xt;
+      }
+    }
+    __syncthreads();
+    const float M = sm_row[0];
+    const float T1 = sm_row[1];
+    const float xt = sm_row[2];
+    const float scale = go / (1.0f + T1);
+    const int64_t lt = target[row];
+    const auto grs = row_rsrc(g + row * ldg);
+    // the target's column relative to this lane's vector 0
+    const int64_t lt0 = lt - static_cast<int64_t>(tid) * EPV;
+    auto write_grad = [&](const u32x4& v, int k) {
+      float f[EPV], y[EPV];
+      E::unpack(v, f);
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
+      set_target_value<EPV>(y, xt, lt0 - k * kBlock * EPV, M, T1, go);
+      __builtin_amdgcn_raw_buffer_store_b128(E::pack(y), grs, voff, k * kBlock * 16,
+                                             kBufNonTemporal);
+    };
+    // The LDS part first, so that the next row's LDS part can stream in
+    // while the register part's gradient is written.
+#pragma unroll
+    for (int k = 0; k < kWideHi; ++k)
+      if (kWideLo + k < cnt) write_grad(hi[k * kBlock + tid], kWideLo + k);
+    __syncthreads();  // every lane is done with this row's LDS part
+    if (next < n_rows) load_hi(next);
+#pragma unroll
+    for (int k = 0; k < kWideLo; ++k)
+      if (k < cnt) write_grad(cur[k], k);
+#pragma unroll
+    for (int k = 0; k < kWideLo; ++k) cur[k] = nxt[k];
+  }
+}
+
 // The backward of an in-place one-pass forward (ce_fwdbwd_kernel with g == x,
 // the logits already overwritten): when the real upstream value gout[0]
 // differs from the assumed[0] the gradient was written for, every entry is
@@ -702,8 +872,8 @@ int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64
 }  // extern "C"
 
 namespace {
-// Workgroups of the one-pass kernel: two per compute unit, each walking rows.
-unsigned one_pass_grid(int64_t n_rows) {
+// Compute units of the current device (256 if the query fails).
+int device_cus() {
   static int cus[64] = {0};
   int dev = 0;
   int n_cu = 256;
@@ -716,9 +886,18 @@ unsigned one_pass_grid(int64_t n_rows) {
     }
     if (cus[dev] > 0) n_cu = cus[dev];
   }
-  const int64_t want = 2 * static_cast<int64_t>(n_cu);
+  return n_cu;
+}
+
+// Workgroups of a kernel that walks rows with `per_cu` workgroups per compute
+// unit, capped by the rows.
+unsigned rows_grid(int64_t n_rows, int per_cu) {
+  const int64_t want = static_cast<int64_t>(per_cu) * device_cus();
   return static_cast<unsigned>(n_rows < want ? n_rows : want);
 }
+
+// Workgroups of the one-pass kernel: two per compute unit, each walking rows.
+unsigned one_pass_grid(int64_t n_rows) { return rows_grid(n_rows, 2); }
 
 int launch_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab_local,
                int64_t ld, int64_t ld_grad, const int64_t* target, int64_t vocab_start,
@@ -792,6 +971,26 @@ void launch_fwdbwd(const void* logits, void* grad, int64_t n_rows, int64_t vocab
                      0, st, static_cast<const T*>(logits), static_cast<T*>(grad), n_rows, vocab,
                      ld, ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, gout_div);
 }
+// One workgroup per compute unit (the LDS part of a row takes 128 KiB).
+template <typename T>
+int launch_fwdbwd_wide(const void* logits, void* grad, int64_t n_rows, int64_t vocab, int64_t ld,
+                       int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
+                       float* g_sumexp_m1, const float* expect, float* assumed, float gout_div,
+                       hipStream_t st) {
+  static bool lds_ok = false;  // the attribute is set once per process and kernel
+  if (!lds_ok) {
+    const hipError_t e =
+        hipFuncSetAttribute(reinterpret_cast<const void*>(&ce_fwdbwd_wide_kernel<T>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kWideLdsBytes);
+    if (e != hipSuccess) return static_cast<int>(e);
+    lds_ok = true;
+  }
+  const unsigned grid = rows_grid(n_rows, 1);
+  hipLaunchKernelGGL((ce_fwdbwd_wide_kernel<T>), dim3(grid), dim3(kStatsBlock), kWideLdsBytes, st,
+                     static_cast<const T*>(logits), static_cast<T*>(grad), n_rows, vocab, ld,
+                     ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, gout_div);
+  return NMCE_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -819,7 +1018,7 @@ int nmce_ce_bwd_scaled_unless(const void* logits, void* grad, int dtype, int64_t
 int64_t nmce_ce_fwd_bwd_max_vocab(int dtype) {
   if (dtype != NMCE_F32 && dtype != NMCE_BF16) return 0;
   const int64_t epv = dtype == NMCE_F32 ? 4 : 8;
-  return epv * kStatsBlock * kOnePassVecs[1];
+  return epv * kStatsBlock * (kWideLo + kWideHi);
 }
 
 int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab,
@@ -841,7 +1040,18 @@ int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, i
       (ld * es) % 16 || (ld_grad * es) % 16)
     return NMCE_EINVAL_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const bool small = (vocab / epv + kStatsBlock - 1) / kStatsBlock <= kOnePassVecs[0];
+  const int64_t per_lane = (vocab / epv + kStatsBlock - 1) / kStatsBlock;
+  if (per_lane > kOnePassVecs[1]) {
+    const int rc = dtype == NMCE_F32
+                       ? launch_fwdbwd_wide<float>(logits, grad, n_rows, vocab, ld, ld_grad, target,
+                                                   loss, g_max, g_sumexp_m1, grad_expected,
+                                                   grad_assumed, gout_div, st)
+                       : launch_fwdbwd_wide<uint16_t>(logits, grad, n_rows, vocab, ld, ld_grad,
+                                                      target, loss, g_max, g_sumexp_m1,
+                                                      grad_expected, grad_assumed, gout_div, st);
+    return rc != NMCE_OK ? rc : launch_status();
+  }
+  const bool small = per_lane <= kOnePassVecs[0];
   if (dtype == NMCE_F32) {
     if (small)
       launch_fwdbwd<float, kOnePassVecs[0]>(logits, grad, n_rows, vocab, ld, ld_grad, target,

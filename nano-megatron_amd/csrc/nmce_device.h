@@ -135,6 +135,14 @@ __device__ __forceinline__ void store_stream(u32x4* p, const u32x4& v) {
   __builtin_nontemporal_store(v, p);
 }
 
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+// MUBUF load of `size` bytes per lane straight into LDS (buffer_load_dwordx4
+// ... lds): SGPR buffer resource, per-lane byte offset, SGPR byte offset; the
+// LDS destination is the wave-uniform `lds` + 16 * lane.
+__device__ void raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) void* lds,
+                                    int size, int voffset, int soffset, int offset,
+                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+
 // ---- wave64 reductions via DPP ---------------------------------------------
 // DPP controls (GFX9): quad_perm, row_half_mirror 0x141, row_mirror 0x140,
 // row_bcast:15 0x142, row_bcast:31 0x143.

@@ -49,14 +49,6 @@
 
 namespace nmce {
 
-typedef int i32x4_t __attribute__((ext_vector_type(4)));
-// MUBUF load of `size` bytes per lane straight into LDS (buffer_load_dwordx4
-// ... lds): SGPR buffer resource, per-lane byte offset, SGPR byte offset; the
-// LDS destination is the wave-uniform `lds` + 16 * lane.
-__device__ void raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) void* lds,
-                                    int size, int voffset, int soffset, int offset,
-                                    int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
-
 namespace {
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));

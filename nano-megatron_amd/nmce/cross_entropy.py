@@ -29,7 +29,8 @@ Differences from the reference, all deliberate:
   place (below), else into a new ``[tokens, vocab]`` buffer. A backward whose
   upstream value differs rewrites a separate buffer from the logits
   (bit-identical to the two-pass path), and rescales an in-place one (within
-  two units in the last place; exact for a power-of-two ratio).
+  four fp32 or two bf16 units in the last place: the written gradient and the
+  ratio are each rounded once; exact for a power-of-two ratio).
   ``one_pass=False`` turns it off.
 * The gradient is written **in place** into the logits storage when the
   logits are a non-leaf tensor (as at model.py:277-281, where they come
@@ -533,8 +534,8 @@ def vocab_parallel_cross_entropy(
     first): in place (the logits hold the gradient once the forward returns)
     or into a new buffer. The backward redoes it only when its upstream value
     differs: bit-identical to the two-pass path, which ``one_pass=False``
-    selects, for a new buffer; rescaled, within two units in the last place,
-    in place. ``upstream_hint`` (a one-element fp32 device tensor) replaces
+    selects, for a new buffer; rescaled, within four fp32 or two bf16 units in
+    the last place, in place. ``upstream_hint`` (a one-element fp32 device tensor) replaces
     the call site's value: the forward assumes what it holds and the backward
     stores what it receives there.
 
