@@ -409,7 +409,8 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": measured_traffic(name, "lmhead_stats_kernel", LMHEAD_TRAFFIC_FILE),
+            "traffic": (measured_traffic(name, "lmhead_p_kernel", LMHEAD_TRAFFIC_FILE)
+                        if one_pass else None),
             "alg_flops_per_launch": flops_per_launch,
             "avg_launch_ms": avg_ms[dominant],
             "launches_per_step": per_step,
