@@ -42,6 +42,8 @@ constexpr int kValidateThreads = 256;
 // Running maxima start here instead of -inf so that rows (or lanes) that have
 // seen only -inf keep finite shifts and 2^(x-m) stays 0 rather than NaN.
 constexpr float kMaxFloor = -1.0e38f;
+// Cache-policy word of the buffer loads and stores: nt (streaming).
+constexpr int kBufNonTemporal = 2;
 
 // Fold K values into a running (m, s) pair, s = sum exp(x - m). (bf16 rows;
 // the lane's t is s - 1 afterwards, exact since s >= 1 once a value is in.)
@@ -260,18 +262,6 @@ __device__ __forceinline__ void set_target(float* y, const T* px, int64_t d, flo
   }
 }
 
-// set_target with the target's logit xt already known (the one-pass kernel
-// broadcasts it before the row is overwritten).
-template <int K>
-__device__ __forceinline__ void set_target_value(float* y, float xt, int64_t d, float M,
-                                                 float T1, float g) {
-  if (static_cast<uint64_t>(d) < static_cast<uint64_t>(K)) {
-    const float yt = target_grad(xt, M, T1, g);
-#pragma unroll
-    for (int k = 0; k < K; ++k) y[k] = (k == d) ? yt : y[k];
-  }
-}
-
 template <typename T, bool kVec, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
 __global__ __launch_bounds__(kBlock) void ce_bwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
@@ -401,15 +391,32 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
 // logits. Each workgroup walks rows blockIdx.x, + gridDim.x, ... and holds a
 // row in registers (at most kVec vectors per lane; rows 16-byte aligned, V a
 // whole number of vectors). It folds the row into (max, sum - 1) in
-// ce_stats_kernel's order and merges exactly as that kernel does, issues the
-// loads of its next row, writes the loss and the statistics, then writes the
-// gradient for the upstream value usable_hint(expect[0]) of the mean (that
-// value / gdiv per token) with ce_bwd_flat_kernel's arithmetic, from the
-// registers; the value used goes to assumed[0]. The target's logit is read
-// once, before any lane writes, and shared through LDS, so g may be x itself
-// (ldg == ld): the row is then overwritten by its gradient. Every output is
-// bit-identical to nmce_ce_fwd followed by nmce_ce_bwd_scaled with that
-// upstream value; the backward runs only when the real value differs.
+// ce_stats_kernel's order, merges exactly as ce_stats_kernel does, writes the
+// loss and the statistics, then writes the gradient for the upstream value
+// usable_hint(expect[0]) of the mean (that value / gdiv per token) with
+// ce_bwd_flat_kernel's arithmetic, from the registers; the value used goes to
+// assumed[0]. Every output is bit-identical to nmce_ce_fwd followed by
+// nmce_ce_bwd_scaled with that upstream value; the backward runs only when the
+// real value differs.
+//
+// The loads of the next row are issued at the top of each row, so they stream
+// in while this row is folded, merged and written. Rows are addressed through
+// buffer resources that span exactly one row, with each lane's whole byte
+// offset in its offset register, which the hardware range-checks: a vector
+// past the row loads as 0 and its store is dropped. So no memory instruction
+// sits in a branch, the compiler can count the outstanding ones exactly, and
+// the fold waits only for its own row, not for the next row's loads or the
+// last row's stores.
+//
+// One barrier per row: every wave merges the waves' pairs itself (the same
+// DPP merge on the same values, so the same bits in every wave), and the
+// pairs are double-buffered by row parity, so a wave that runs ahead into the
+// next row cannot overwrite pairs another wave is still reading. The target's
+// logit is read by every lane (one address) at the top of the row, before any
+// lane writes the row, so g may be x itself (ldg == ld): the row is then
+// overwritten by its gradient. The target column is written by the lane whose
+// vector holds it, as one element after that vector: no lane tests its
+// vectors for the target.
 template <typename T, int kVec, int kBlock = kStatsBlock>
 __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
@@ -423,27 +430,42 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
   static_assert(kVec % 2 == 0, "vectors are folded in pairs");
   const float expect = usable_hint(expect_in[0]);
   if (blockIdx.x == 0 && threadIdx.x == 0) assumed[0] = expect;
-  __shared__ float sm_m[kWaves];
-  __shared__ float sm_s[kWaves];
-  __shared__ float sm_row[3];
+  __shared__ float sm_m[2][kWaves];
+  __shared__ float sm_s[2][kWaves];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int64_t nvec = V / EPV;
+  const int row_bytes = static_cast<int>(nvec * 16);
   const float go = expect / gdiv;
+  // A resource over row r (no bytes when r is past the last row, so that
+  // every load through it reads 0 and touches no memory).
+  auto rsrc = [&](const T* base, int64_t r, int64_t stride) {
+    const bool live = r < n_rows;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(live ? base + r * stride : base), 0,
+                                             live ? row_bytes : 0, 0x00020000);
+  };
+  auto voff = [&](int k) { return static_cast<uint32_t>(tid + k * kBlock) * 16u; };
   u32x4 cur[kVec], nxt[kVec];
   auto load_row = [&](int64_t r, u32x4* v) {
-    const u32x4* vp = reinterpret_cast<const u32x4*>(x + r * ld);
+    const auto rs = rsrc(x, r, ld);
 #pragma unroll
-    for (int k = 0; k < kVec; ++k) {
-      const int64_t i = tid + static_cast<int64_t>(k) * kBlock;
-      if (i < nvec) v[k] = load_stream(vp + i);
-    }
+    for (int k = 0; k < kVec; ++k)
+      v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff(k), 0, kBufNonTemporal);
   };
   int64_t row = blockIdx.x;
-  if (row < n_rows) load_row(row, cur);
-  for (; row < n_rows; row += gridDim.x) {
-    const T* xr = x + row * ld;
+  load_row(row, cur);
+  for (int parity = 0; row < n_rows; row += gridDim.x, parity ^= 1) {
+    const auto rx = rsrc(x, row, ld);
+    // A target outside [0, V) (the host's check reports it after the launch)
+    // picks nothing, as in ce_stats_kernel. The offset stays inside the row
+    // either way (the compiler may put a uniform offset where it is not
+    // range-checked).
+    const int64_t lt = target[row];
+    const bool owned = lt >= 0 && lt < V;
+    const uint32_t lt_off = owned ? static_cast<uint32_t>(lt) * sizeof(T) : 0u;
+    const float xt_raw = E::buf_load1(rx, lt_off);
+    load_row(row + gridDim.x, nxt);
     // ce_stats_kernel's order: vectors k and k + 1 (kBlock apart) together
     // while both exist, then the one left, if any.
     float m = kMaxFloor, a = kExact ? -1.0f : 0.0f;
@@ -465,55 +487,42 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
         }
       }
     }
-    // The next row streams in while this one is merged and written.
-    const int64_t next = row + gridDim.x;
-    if (next < n_rows) load_row(next, nxt);
     float t = kExact ? a : a - 1.0f;
     wave_merge_excess(m, t);
     if (lane == 0) {
-      sm_m[wave] = m;
-      sm_s[wave] = t;
+      sm_m[parity][wave] = m;
+      sm_s[parity][wave] = t;
     }
     __syncthreads();
-    if (wave == 0) {
-      float M = lane < kWaves ? sm_m[lane] : kMaxFloor;
-      float T1 = lane < kWaves ? sm_s[lane] : -1.0f;
-      wave_merge_excess(M, T1);
-      if (lane == 0) {
-        // A target outside [0, V) (the host's check reports it after the
-        // launch) picks nothing, as in ce_stats_kernel.
-        const int64_t lt = target[row];
-        const float xt = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
-        out_max[row] = M;
-        out_sum1[row] = T1;
-        loss[row] = log1pf(T1) - (xt - M);
-        sm_row[0] = M;
-        sm_row[1] = T1;
-        sm_row[2] = xt;
-      }
+    float M = lane < kWaves ? sm_m[parity][lane] : kMaxFloor;
+    float T1 = lane < kWaves ? sm_s[parity][lane] : -1.0f;
+    wave_merge_excess(M, T1);
+    const float xt = owned ? xt_raw : 0.0f;
+    if (tid == 0) {
+      out_max[row] = M;
+      out_sum1[row] = T1;
+      loss[row] = log1pf(T1) - (xt - M);
     }
-    __syncthreads();
-    const float M = sm_row[0];
-    const float T1 = sm_row[1];
-    const float xt = sm_row[2];
     const float scale = go / (1.0f + T1);
-    const int64_t lt = target[row];
-    T* gr = g + row * ldg;
+    const auto rg = rsrc(g, row, ldg);
 #pragma unroll
     for (int k = 0; k < kVec; ++k) {
-      const int64_t i = tid + static_cast<int64_t>(k) * kBlock;
-      if (i < nvec) {
+      u32x4 out = {0u, 0u, 0u, 0u};
+      if (tid + static_cast<int64_t>(k) * kBlock < nvec) {
         float f[EPV], y[EPV];
         E::unpack(cur[k], f);
 #pragma unroll
         for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
-        set_target_value<EPV>(y, xt, lt - i * EPV, M, T1, go);
-        store_stream(reinterpret_cast<u32x4*>(gr) + i, E::pack(y));
+        out = E::pack(y);
       }
+      __builtin_amdgcn_raw_buffer_store_b128(out, rg, voff(k), 0, kBufNonTemporal);
     }
+    // Every lane stores; only the owner's offset is inside the row.
+    const bool mine = owned && (lt / EPV) % kBlock == tid;
+    E::buf_store1(target_grad(xt, M, T1, go), rg,
+                  mine ? static_cast<uint32_t>(lt) * sizeof(T) : static_cast<uint32_t>(row_bytes));
 #pragma unroll
     for (int k = 0; k < kVec; ++k) cur[k] = nxt[k];
-    __syncthreads();  // sm_row is rewritten for the next row
   }
 }
 
@@ -526,8 +535,6 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
 // next row's register part is loaded right after this row's fold. Same fold
 // order, merges and per-element arithmetic as ce_fwdbwd_kernel (and so as
 // ce_stats_kernel and ce_bwd_flat_kernel): bit-identical outputs.
-// Cache-policy word of the buffer loads and stores: nt (streaming).
-constexpr int kBufNonTemporal = 2;
 constexpr int kWideLo = 7;
 constexpr int kWideHi = 9;
 constexpr int kWideLdsBytes = kWideHi * kStatsBlock * 16;  // 144 KiB
@@ -551,7 +558,6 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
   if (blockIdx.x == 0 && threadIdx.x == 0) assumed[0] = expect;
   __shared__ float sm_m[kWaves];
   __shared__ float sm_s[kWaves];
-  __shared__ float sm_row[3];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -600,6 +606,11 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
   }
   for (; row < n_rows; row += gridDim.x) {
     const T* xr = x + row * ld;
+    // The target's logit, read by every lane (one address) before any lane
+    // writes the row; a target outside [0, V) picks nothing.
+    const int64_t lt = target[row];
+    const bool owned = lt >= 0 && lt < V;
+    const float xt = owned ? E::load1(xr + lt) : 0.0f;
     // ce_stats_kernel's order: vectors k and k + 1 (kBlock apart) together
     // while both exist, then the one left, if any. Vectors below kWideLo
     // come from registers, the rest from LDS once every wave's loads of this
@@ -638,37 +649,24 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
       sm_s[wave] = t;
     }
     __syncthreads();
-    if (wave == 0) {
-      float M = lane < kWaves ? sm_m[lane] : kMaxFloor;
-      float T1 = lane < kWaves ? sm_s[lane] : -1.0f;
-      wave_merge_excess(M, T1);
-      if (lane == 0) {
-        // A target outside [0, V) picks nothing, as in ce_stats_kernel.
-        const int64_t lt = target[row];
-        const float xt = (lt >= 0 && lt < V) ? E::load1(xr + lt) : 0.0f;
-        out_max[row] = M;
-        out_sum1[row] = T1;
-        loss[row] = log1pf(T1) - (xt - M);
-        sm_row[0] = M;
-        sm_row[1] = T1;
-        sm_row[2] = xt;
-      }
+    // Every wave merges the waves' pairs itself (the same DPP merge on the
+    // same values, so the same bits in every wave). The next writes of the
+    // pairs come after two more barriers of this row.
+    float M = lane < kWaves ? sm_m[lane] : kMaxFloor;
+    float T1 = lane < kWaves ? sm_s[lane] : -1.0f;
+    wave_merge_excess(M, T1);
+    if (tid == 0) {
+      out_max[row] = M;
+      out_sum1[row] = T1;
+      loss[row] = log1pf(T1) - (xt - M);
     }
-    __syncthreads();
-    const float M = sm_row[0];
-    const float T1 = sm_row[1];
-    const float xt = sm_row[2];
     const float scale = go / (1.0f + T1);
-    const int64_t lt = target[row];
     const auto grs = row_rsrc(g + row * ldg);
-    // the target's column relative to this lane's vector 0
-    const int64_t lt0 = lt - static_cast<int64_t>(tid) * EPV;
     auto write_grad = [&](const u32x4& v, int k) {
       float f[EPV], y[EPV];
       E::unpack(v, f);
 #pragma unroll
       for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
-      set_target_value<EPV>(y, xt, lt0 - k * kBlock * EPV, M, T1, go);
       __builtin_amdgcn_raw_buffer_store_b128(E::pack(y), grs, voff, k * kBlock * 16,
                                              kBufNonTemporal);
     };
@@ -682,6 +680,10 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
 #pragma unroll
     for (int k = 0; k < kWideLo; ++k)
       if (k < cnt) write_grad(cur[k], k);
+    // The target column, by the lane whose vector holds it, after that vector
+    // (through the same resource; the owner's offset is inside the row).
+    if (owned && (lt / EPV) % kBlock == tid)
+      E::buf_store1(target_grad(xt, M, T1, go), grs, static_cast<uint32_t>(lt) * sizeof(T));
 #pragma unroll
     for (int k = 0; k < kWideLo; ++k) cur[k] = nxt[k];
   }
@@ -896,7 +898,11 @@ unsigned rows_grid(int64_t n_rows, int per_cu) {
   return static_cast<unsigned>(n_rows < want ? n_rows : want);
 }
 
-// Workgroups of the one-pass kernel: two per compute unit, each walking rows.
+// Workgroups of the one-pass kernel, each walking rows: two per compute unit
+// (one resident at a time where its registers allow only one; the second
+// half starts as the first finishes, measured 0.7% faster than one per unit
+// at [16384, 50304] bf16). The backward kernels that follow it (they exit
+// at once when the upstream value matches) use the same grid.
 unsigned one_pass_grid(int64_t n_rows) { return rows_grid(n_rows, 2); }
 
 int launch_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab_local,

@@ -107,6 +107,15 @@ struct Elem<float> {
   }
   __device__ static __forceinline__ float load1(const float* p) { return *p; }
   __device__ static __forceinline__ void store1(float* p, float v) { *p = v; }
+  // One element at byte offset `off` through a buffer resource (an offset
+  // past the resource's range reads 0 / stores nothing).
+  __device__ static __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  }
+  __device__ static __forceinline__ void buf_store1(float v, __amdgpu_buffer_rsrc_t r,
+                                                    uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, off, 0, 0);
+  }
 };
 
 template <>
@@ -124,6 +133,13 @@ struct Elem<uint16_t> {  // bf16 storage
   }
   __device__ static __forceinline__ float load1(const uint16_t* p) { return bf16_to_f32(*p); }
   __device__ static __forceinline__ void store1(uint16_t* p, float v) { *p = f32_to_bf16(v); }
+  __device__ static __forceinline__ float buf_load1(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return bf16_to_f32(__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0));
+  }
+  __device__ static __forceinline__ void buf_store1(float v, __amdgpu_buffer_rsrc_t r,
+                                                    uint32_t off) {
+    __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16(v), r, off, 0, 0);
+  }
 };
 
 // Streaming 16-byte loads: the logit slab is read once per pass and is far
