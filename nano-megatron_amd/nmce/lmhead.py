@@ -71,10 +71,21 @@ DEFAULT_VOCAB_CHUNK = 32768
 # either way.
 BACKWARD_GEMM = "nmce"
 
-# Tokens per chunk of the one-pass path: each chunk holds its exponentials and
-# its dZ in both layouts, 4 * chunk * V bytes (bf16), so no tensor the size of
-# the full logits exists; with more than one chunk dW is accumulated in fp32.
-DEFAULT_TOKEN_CHUNK = 8192
+# Bytes the one-pass path may hold for one chunk of tokens: the chunk's
+# exponentials and its dZ, 4 * chunk * V bytes (bf16). The default chunk is
+# the most tokens (a multiple of 256) within this budget, all of them when they
+# fit: a 16384-token micro-batch at V = 256000 takes 15.6 GiB of a 288 GB
+# device, less than the reference's fp32 logits and softmax for the same
+# tokens. One chunk needs no fp32 accumulation of dW across chunks, which cost
+# 3% of the step at [16384, 4096] x [128256, 4096] and 10% at
+# [16384, 3072] x [256000, 3072] (two chunks of 8192 against one of 16384).
+CHUNK_BUDGET_BYTES = 16 << 30
+
+
+def default_token_chunk(n_tokens: int, vocab_local: int) -> int:
+    """Tokens per one-pass chunk within ``CHUNK_BUDGET_BYTES``."""
+    fit = CHUNK_BUDGET_BYTES // (4 * max(1, vocab_local)) // 256 * 256
+    return n_tokens if fit >= n_tokens else max(256, fit)
 
 _ALIGN = 64  # hidden size granularity of the GEMM kernels
 
@@ -228,7 +239,7 @@ class _LMHeadVocabParallelCrossEntropyMean(torch.autograd.Function):
             ctx.weight_shape = weight.shape
             return torch.empty(0, dtype=torch.float32, device=dev).mean()
         ctx.empty = False
-        chunk = DEFAULT_TOKEN_CHUNK if token_chunk is None else int(token_chunk)
+        chunk = default_token_chunk(n, V) if token_chunk is None else int(token_chunk)
         L = _fused_layout(lib, n, hp, V, chunk)
         ws = _workspace(L["total"], dev)
         args = (x.data_ptr(), w.data_ptr(), _lib.NMCE_BF16, n, hp, V)
@@ -433,7 +444,7 @@ def lmhead_vocab_parallel_cross_entropy(
 
     When a gradient is wanted the forward is one pass (module docstring),
     going through ``token_chunk`` tokens at a time (default
-    ``DEFAULT_TOKEN_CHUNK``) and assuming the upstream value held by
+    ``default_token_chunk``: every token, within ``CHUNK_BUDGET_BYTES``) and assuming the upstream value held by
     ``upstream_hint`` (a one-element fp32 device tensor; default: one per
     call site). ``one_pass=False`` selects the forward that keeps only the
     row statistics, with a backward that recomputes the logits in chunks of
@@ -510,7 +521,7 @@ class FusedParallelLMHead(torch.nn.Module):
         self.weight.tensor_parallel_sharded = True
         self.sequence_parallel = bool(getattr(config, "sequence_parallel", False))
         self.vocab_chunk = None  # backward chunk; None = DEFAULT_VOCAB_CHUNK
-        self.token_chunk = None  # one-pass chunk; None = DEFAULT_TOKEN_CHUNK
+        self.token_chunk = None  # one-pass chunk; None = default_token_chunk
         # The upstream value the one-pass forward assumes, per module and
         # device (created on first use on that device).
         self._hints: dict = {}

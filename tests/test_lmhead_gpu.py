@@ -614,17 +614,18 @@ def _lse_all(xd, wd, chunk=1024):
     return torch.cat(out)
 
 
-@pytest.mark.parametrize("route", ["one_pass", "library", "nmce"])
+@pytest.mark.parametrize("route", ["one_pass", "one_pass_chunked", "library", "nmce"])
 @pytest.mark.parametrize("cfg", ["c4", "c5"])
 def test_fused_workload(cfg, route, monkeypatch):
     """c4: hidden [16384, 4096] ~ N(0,1), W [128256, 4096] ~ N(0, 0.02^2), uniform
     targets. c5: hidden [16384, 3072], W [256000, 3072] ~ N(0, 0.05^2) with 64
     rows x30, Zipf(1.1) targets (logits far beyond +-60). Every route: the
-    drop-in's default one-pass path (two chunks of 8192 tokens, dW
-    accumulated in fp32 across them; the mean loss equal to the per-token
-    Function's, bit for bit), and the recomputing backward through the
-    library's products or the hand-written one (dX accumulated in fp32 over
-    the 32768-row vocabulary chunks, 4 at c4, 8 at c5)."""
+    drop-in's default one-pass path (one chunk of all 16384 tokens; the mean
+    loss equal to the per-token Function's, bit for bit), the same in two
+    chunks of 8192 tokens (dW accumulated in fp32 across them), and the
+    recomputing backward through the library's products or the hand-written
+    one (dX accumulated in fp32 over the 32768-row vocabulary chunks, 4 at c4,
+    8 at c5)."""
     import nmce
     from nmce import lmhead as lm
     monkeypatch.setattr(lm, "BACKWARD_GEMM", route)
@@ -648,10 +649,11 @@ def test_fused_workload(cfg, route, monkeypatch):
     ctx = nmce.ParallelContext.single()
     xd = x.clone().requires_grad_(True)
     wd = w.clone().requires_grad_(True)
-    if route == "one_pass":
+    if route.startswith("one_pass"):
         hint = torch.ones(1, dtype=torch.float32, device=DEV)
+        chunk = 8192 if route == "one_pass_chunked" else None
         loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t, 0, v, ctx,
-                                                        upstream_hint=hint)
+                                                        token_chunk=chunk, upstream_hint=hint)
         loss.backward()
         with torch.no_grad():
             per_tok = nmce._LMHeadVocabParallelCrossEntropy.apply(x, w, t, 0, v, None, 1, None)
