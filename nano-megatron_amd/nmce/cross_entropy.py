@@ -19,7 +19,7 @@ Differences from the reference, all deliberate:
   and softmax - 1 give the same values up to fp32 cancellation near 1.
 * The wrapper at TP = 1, when a gradient is wanted (grad mode on and the
   logits require grad) and the rows fit (V a whole number of 16-byte
-  vectors, at most 65536 bf16 / 32768 fp32 columns), reads the logits once:
+  vectors, at most 131072 bf16 / 65536 fp32 columns), reads the logits once:
   its forward also writes the gradient for the upstream value that the last
   backward from the same call site received (1.0, as for
   ``loss.backward()``, before the first) -- as the reference's forward
@@ -141,6 +141,11 @@ def _check_inputs(logits: torch.Tensor, target: torch.Tensor, vocab_start: int,
             f"[{vocab_start}, {vocab_end}) has {vocab_end - vocab_start}")
 
 
+# Event queries (about a microsecond each) before the target check falls back
+# to a blocking wait.
+_CHECK_POLLS = 200
+
+
 class _PendingCheck:
     """Bad-target counts on their way to pinned host memory."""
 
@@ -149,7 +154,15 @@ class _PendingCheck:
         self.event = event
 
     def raise_if_bad(self) -> None:
-        self.event.synchronize()
+        # The counts usually reach the host within microseconds of the call:
+        # poll first, so that a blocking wait's wake-up latency (tens of
+        # microseconds, per step of a small batch) is paid only by long waits.
+        event = self.event
+        for _ in range(_CHECK_POLLS):
+            if event.query():
+                break
+        else:
+            event.synchronize()
         if int(self.host.sum()) != 0:
             raise ValueError("target token id is outside the model vocabulary")
 
