@@ -115,8 +115,17 @@ def dtype_code(dtype: torch.dtype) -> int:
     raise TypeError(f"unsupported logits dtype {dtype}; expected float32 or bfloat16")
 
 
+# torch's raw-stream query (what its compiled kernels' launchers call): a
+# fraction of the cost of building a Stream object per launch, which matters
+# for small batches, where a step is a few microseconds of GPU work.
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_handle(device: torch.device) -> int:
     """The raw hipStream_t of torch's current stream on ``device``."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
 

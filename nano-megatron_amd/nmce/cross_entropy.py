@@ -198,19 +198,22 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
     if n == 0:
         return None
     slots = lib.nmce_validate_slots(n)
-    main = torch.cuda.current_stream(t.device)
     if not on_side_stream:
         # On the loss stream, ahead of a kernel that fills every compute unit
         # for its whole run (the one-pass forward), so that the host's wait
         # ends early instead of after that kernel.
         counts = torch.empty(slots, dtype=torch.int32, device=t.device)
         _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
-                vocab_size, counts.data_ptr(), main.cuda_stream)
+                vocab_size, counts.data_ptr(), _lib.stream_handle(t.device))
         host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
         host.copy_(counts, non_blocking=True)
         event = torch.cuda.Event()
-        event.record(main)
+        if t.device.index is None or t.device.index == torch.cuda.current_device():
+            event.record()  # the current device's current stream
+        else:
+            event.record(torch.cuda.current_stream(t.device))
         return _PendingCheck(host, event)
+    main = torch.cuda.current_stream(t.device)
     side = _side_stream(t.device)
     side.wait_stream(main)  # the targets are complete in the current stream's order
     with torch.cuda.stream(side):
@@ -329,9 +332,17 @@ def _one_pass_rows(logits: torch.Tensor, world_size: int) -> torch.Tensor | None
     ld = rows.stride(0) if rows.shape[0] > 1 else V
     if (V * es) % 16 or (ld * es) % 16 or rows.data_ptr() % 16:
         return None
-    if V > _lib.load().nmce_ce_fwd_bwd_max_vocab(_lib.dtype_code(rows.dtype)):
+    code = _lib.dtype_code(rows.dtype)
+    limit = _one_pass_limit.get(code)
+    if limit is None:
+        limit = _one_pass_limit[code] = int(_lib.load().nmce_ce_fwd_bwd_max_vocab(code))
+    if V > limit:
         return None
     return rows
+
+
+# The one-pass kernel's widest row per dtype code (a property of the library).
+_one_pass_limit: dict[int, int] = {}
 
 
 def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint, inplace):
@@ -541,7 +552,7 @@ def vocab_parallel_cross_entropy(
 
     At TP = 1, when a gradient is wanted (grad mode on, logits requiring grad)
     and the rows fit the one-pass kernel (V a whole number of 16-byte vectors,
-    at most 65536 bf16 or 32768 fp32 columns, rows 16-byte aligned), the
+    at most 131072 bf16 or 65536 fp32 columns, rows 16-byte aligned), the
     forward reads the logits once and also writes their gradient, for the
     upstream value the previous backward of this call site received (1.0 at
     first): in place (the logits hold the gradient once the forward returns)
