@@ -680,8 +680,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
 // 0 (pt holds 0 there), tokens past N are not written to dz.
 // ---------------------------------------------------------------------------
 constexpr int kRsRows = kPartialRows;  // 128: one block of partial statistics
-constexpr int kRsToks = 64;
-
+constexpr int kRsToks = 128;
 __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
     uint16_t* __restrict__ pt, int64_t ldt, uint16_t* __restrict__ dz, int64_t ldz, int64_t V,
     int64_t N, const float* __restrict__ pmax, int64_t nb, const float* __restrict__ gmax,
@@ -691,8 +690,11 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
   __shared__ float s_scale[kRsToks];
   __shared__ float s_dt[kRsToks];
   __shared__ int s_tv[kRsToks];
-  // token-major copy of the tile for the dz stores; rows padded by 16 bytes
-  __shared__ __align__(16) uint16_t tile[kRsToks][kRsRows + 8];
+  // The tile, token-major, as words of two vocabulary rows: word q of token
+  // t holds rows 2q (low half) and 2q + 1 (high half), at t * 64 +
+  // (q ^ 4 ((t >> 3) & 15)). The XOR spreads both the word writes of the pt
+  // pass and the 16-byte reads of the dz pass over all 64 banks.
+  __shared__ __align__(16) uint32_t tile[kRsToks * (kRsRows / 2)];
   const int64_t blk = blockIdx.x;
   const int64_t v0 = blk * kRsRows;
   const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kRsToks;
@@ -716,15 +718,15 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
     s_tv[tid] = tv;
   }
   __syncthreads();
-  // pt: 128 rows x 64 tokens, 8 vectors of 8 tokens per row.
-#pragma unroll
-  for (int it = 0; it < kRsRows * (kRsToks / 8) / 256; ++it) {
-    const int lin = it * 256 + tid;
-    const int r = lin / (kRsToks / 8);
-    const int tg = 8 * (lin % (kRsToks / 8));
-    u32x4* p = reinterpret_cast<u32x4*>(pt + (v0 + r) * ldt + t0 + tg);
-    float f[8];
-    Elem<uint16_t>::unpack(*p, f);
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  // pt pass: a lane takes tokens 8s .. 8s + 7 of two adjacent rows per
+  // iteration; a wave's load covers four rows' 256-byte segments. The last
+  // tile of a row may stop at ldt (a multiple of 64) halfway.
+  const int sg = lane & 15;
+  const int tg = 8 * sg;
+  const bool tok_ok = t0 + tg < ldt;
+  auto fix = [&](float* f, int r) {
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       // A zero factor (padding, or an exponential that underflows) writes 0
@@ -734,25 +736,51 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
       f[k] = c == 0.0f ? 0.0f : f[k] * c;
       f[k] = (s_tv[tg + k] == r) ? s_dt[tg + k] : f[k];
     }
-    const u32x4 w = Elem<uint16_t>::pack(f);
-    *p = w;
-    const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+  };
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      tile[tg + 2 * k][r] = static_cast<uint16_t>(ws[k] & 0xffffu);
-      tile[tg + 2 * k + 1][r] = static_cast<uint16_t>(ws[k] >> 16);
+  for (int it = 0; it < kRsRows / 2 / 16; ++it) {
+    const int q = (lane >> 4) + 4 * (wave + 4 * it);  // row pair
+    const int r = 2 * q;
+    u32x4* p0 = reinterpret_cast<u32x4*>(pt + (v0 + r) * ldt + t0 + tg);
+    u32x4* p1 = reinterpret_cast<u32x4*>(pt + (v0 + r + 1) * ldt + t0 + tg);
+    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
+    if (tok_ok) {
+      a = *p0;
+      b = *p1;
+    }
+    float fa[8], fb[8];
+    Elem<uint16_t>::unpack(a, fa);
+    Elem<uint16_t>::unpack(b, fb);
+    fix(fa, r);
+    fix(fb, r + 1);
+    const u32x4 wa = Elem<uint16_t>::pack(fa);
+    const u32x4 wb = Elem<uint16_t>::pack(fb);
+    if (tok_ok) {
+      *p0 = wa;
+      *p1 = wb;
+    }
+    const uint32_t la[4] = {wa.x, wa.y, wa.z, wa.w};
+    const uint32_t lb[4] = {wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t lo = (k & 1) ? (la[k >> 1] >> 16) : (la[k >> 1] & 0xffffu);
+      const uint32_t hi = (k & 1) ? (lb[k >> 1] & 0xffff0000u) : (lb[k >> 1] << 16);
+      const int t = tg + k;
+      tile[t * 64 + (q ^ (4 * ((t >> 3) & 15)))] = lo | hi;
     }
   }
   __syncthreads();
-  // dz: 64 token rows x 128 vocabulary entries, 16 vectors per row.
+  // dz pass: token rows of 128 vocabulary entries (16 chunks of 16 bytes); a
+  // wave's store covers four tokens' 256-byte segments.
 #pragma unroll
-  for (int it = 0; it < kRsToks * (kRsRows / 8) / 256; ++it) {
-    const int lin = it * 256 + tid;
-    const int t = lin / (kRsRows / 8);
-    const int vg = 8 * (lin % (kRsRows / 8));
-    if (t0 + t < N)
-      *reinterpret_cast<u32x4*>(dz + (t0 + t) * ldz + v0 + vg) =
-          *reinterpret_cast<const u32x4*>(&tile[t][vg]);
+  for (int it = 0; it < kRsToks / 16; ++it) {
+    const int t = (lane >> 4) + 4 * (wave + 4 * it);
+    const int w = lane & 15;
+    if (t0 + t < N) {
+      const int sw = (t >> 3) & 15;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[t * 64 + 4 * (w ^ sw)]);
+      *reinterpret_cast<u32x4*>(dz + (t0 + t) * ldz + v0 + 8 * w) = v;
+    }
   }
 }
 
@@ -1340,7 +1368,7 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
   // dZ of the chunk, vocabulary-major in place of P^T and token-major into dz.
   hipLaunchKernelGGL(lmhead_dz_rescale_kernel,
                      dim3(static_cast<unsigned>(L.vpad / kRsRows),
-                          static_cast<unsigned>(L.ldt / kRsToks)),
+                          static_cast<unsigned>((L.ldt + kRsToks - 1) / kRsToks)),
                      dim3(256), 0, s, pt, L.ldt, dz, L.vpad, V, nc, pmax, L.nb, g_max + t0,
                      g_sumexp_m1 + t0, target_logit + t0, target + t0, vocab_start,
                      grad_output + t0 * gout_stride, gout_stride, gout_div);
