@@ -675,7 +675,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
 // and, on the target row, (softmax - 1) * g from the fp32 target logit
 // (target_grad). Written in place into pt (vocabulary-major, the dW GEMM's A)
 // and transposed into dz [N, ldz] (token-major, the dX GEMM's A). A workgroup
-// takes one 128-row block of partial statistics and 64 tokens; the factor of
+// takes one 128-row block of partial statistics and 128 tokens; the factor of
 // each (block, token) is formed once. Rows past V and blocks past nb come out
 // 0 (pt holds 0 there), tokens past N are not written to dz.
 // ---------------------------------------------------------------------------
