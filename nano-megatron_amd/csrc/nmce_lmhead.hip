@@ -17,6 +17,16 @@
 //             dW_c   = dZ^T_c X      (M = Vc, N = hidden, K = tokens; B = X^T)
 //             dX    += dZ_c W_c      (M = tokens, N = hidden, K = Vc; B = W^T)
 //
+// The one-pass path (the drop-in's default) computes Z once, per chunk of
+// tokens (all of them when the chunk's buffers fit the caller's budget):
+//             P^T  = exp(W X^T - block max), bf16, with the partial statistics
+//             dZ^T = P^T * exp(block max - M) * g / S - onehot, in place, and
+//                    its transpose dZ (once the statistics are combined)
+//             dX   = dZ W            (via W^T, K = vocab)
+//             dW  += dZ^T X          (via X^T, K = the chunk's tokens; fp32
+//                                     across chunks only when there are several)
+// so 6 N V H flops in all, against 8 N V H for the recomputing backward.
+//
 // Tokens are the MFMA N dimension in the loss GEMMs: the 32x32 accumulator
 // gives each lane 16 vocabulary rows of a single token, so the per-token
 // reductions are mostly in-register, with one cross-half shuffle.
@@ -68,9 +78,9 @@ constexpr int kWavesM = NMCE_LMHEAD_WAVES_M;
 constexpr int kWavesN = NMCE_LMHEAD_WAVES_N;
 constexpr int kThreads = 64 * kWavesM * kWavesN;
 constexpr int kWaveM = kBM / kWavesM;  // 128
-constexpr int kWaveN = kBN / kWavesN;  // 128
+constexpr int kWaveN = kBN / kWavesN;  // 64
 constexpr int kFM = kWaveM / 32;       // 4 accumulators down
-constexpr int kFN = kWaveN / 32;       // 4 accumulators across
+constexpr int kFN = kWaveN / 32;       // 2 accumulators across
 constexpr int kStageA = kBM * kBK * 2;  // bytes
 constexpr int kStageB = kBN * kBK * 2;
 constexpr int kStage = kStageA + kStageB;
