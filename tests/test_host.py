@@ -131,6 +131,34 @@ def test_default_chunk_never_holds_full_logits(lib):
         assert buf[4] == 1
 
 
+def test_one_pass_token_chunk_budget(lib):
+    """The one-pass path's default token chunk: every token while the chunk's
+    exponentials and dZ (4 V bytes per token) fit the budget, else the most
+    multiples of 256 that do; the fused layout then holds one chunk (no fp32
+    dW accumulator) or several (with one)."""
+    import ctypes
+    from nmce import _lib as L
+    from nmce import lmhead
+    budget = lmhead.CHUNK_BUDGET_BYTES
+    chunk = lmhead.default_token_chunk
+    assert chunk(16384, 128256) == 16384 and chunk(16384, 256000) == 16384
+    for n, v in ((65536, 256000), (1 << 20, 128256), (40000, 1000000)):
+        c = chunk(n, v)
+        assert c < n and c % 256 == 0
+        assert 4 * v * c <= budget < 4 * v * (c + 256)
+    assert chunk(100, 1 << 40) == 256  # at least one tile column
+    buf = (ctypes.c_int64 * L.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
+    # fields: total, chunk, n_chunks, ldt, vpad, nb, off_wt, off_xt, off_pt, off_dz, off_part, off_acc
+    assert lib.nmce_lmhead_ce_fused_layout(16384, 4096, 128256, chunk(16384, 128256),
+                                           ctypes.addressof(buf)) == 0
+    assert (buf[1], buf[2]) == (16384, 1) and buf[11] == buf[0]  # no accumulator region
+    n, v = 65536, 256000
+    assert lib.nmce_lmhead_ce_fused_layout(n, 3072, v, chunk(n, v), ctypes.addressof(buf)) == 0
+    assert buf[2] > 1 and buf[0] - buf[11] >= v * 3072 * 4  # fp32 dW accumulator
+    regions = [buf[6], buf[7], buf[8], buf[9], buf[10], buf[11]]
+    assert all(r % 256 == 0 for r in regions) and regions == sorted(regions)
+
+
 def test_validate_slots(lib):
     assert lib.nmce_validate_slots(0) == 0
     assert lib.nmce_validate_slots(1) == 1
