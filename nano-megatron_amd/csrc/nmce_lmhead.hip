@@ -547,6 +547,60 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
   const int wave = threadIdx.x >> 6;
   const int wm = wave / kWavesN, wn = wave % kWavesN;
   const int fhalf = lane >> 5;
+  if constexpr (kMode == 0) {
+    // bf16 out through the freed LDS, as lmhead_p_kernel stages P^T: words
+    // of two rows (vp = row / 2) per column, columns XOR-swizzled by the row
+    // pair, then 16-byte stores of 512-byte row segments. Tiles that reach
+    // past N, and outputs that are not 16-byte aligned, store element by
+    // element.
+    const bool vec_ok = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0;
+    __syncthreads();  // every wave is done with the operand buffers
+    uint32_t* P = reinterpret_cast<uint32_t*>(lds);
+    auto pcol = [](int vp, int t) { return t ^ (((vp >> 2) & 15) << 2); };
+#pragma unroll
+    for (int fn = 0; fn < kFN; ++fn) {
+      const int cloc = wn * kWaveN + 32 * fn + (lane & 31);
+#pragma unroll
+      for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int vp = (wm * kWaveM + 32 * fm + 8 * q + 4 * fhalf) >> 1;
+          const int col = pcol(vp, cloc);
+          P[vp * kBN + col] = pack_bf16x2(acc.c[fm][fn][4 * q], acc.c[fm][fn][4 * q + 1]);
+          P[(vp + 1) * kBN + col] =
+              pack_bf16x2(acc.c[fm][fn][4 * q + 2], acc.c[fm][fn][4 * q + 3]);
+        }
+    }
+    __syncthreads();
+#pragma unroll 2
+    for (int it = 0; it < (kBM / 2) * (kBN / 8) / kThreads; ++it) {
+      const int lin = it * kThreads + static_cast<int>(threadIdx.x);
+      const int vp = lin / (kBN / 8);
+      const int c0 = 8 * (lin % (kBN / 8));
+      const u32x4 a = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, c0));
+      const u32x4 b = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, c0 + 4));
+      const u32x4 lo = {(a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
+                        (b.x & 0xffffu) | (b.y << 16), (b.z & 0xffffu) | (b.w << 16)};
+      const u32x4 hi = {(a.x >> 16) | (a.y & 0xffff0000u), (a.z >> 16) | (a.w & 0xffff0000u),
+                        (b.x >> 16) | (b.y & 0xffff0000u), (b.z >> 16) | (b.w & 0xffff0000u)};
+      const int64_t col0 = n0 + c0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t row = m0 + 2 * vp + h;
+        if (row >= M || col0 >= N) continue;
+        const u32x4 w = h ? hi : lo;
+        uint16_t* dst = C + row * ldc + col0;
+        if (vec_ok && col0 + 8 <= N) {
+          *reinterpret_cast<u32x4*>(dst) = w;
+        } else {
+          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+          for (int e = 0; e < 8 && col0 + e < N; ++e)
+            dst[e] = static_cast<uint16_t>(e & 1 ? ws[e >> 1] >> 16 : ws[e >> 1] & 0xffffu);
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int fn = 0; fn < kFN; ++fn) {
     const int64_t col = n0 + wn * kWaveN + 32 * fn + (lane & 31);
