@@ -22,6 +22,8 @@ per shard (tolerances in the docstrings).
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -350,3 +352,79 @@ def test_fused_extreme_inputs(case):
     np.testing.assert_allclose(loss, rl, rtol=1e-5, atol=max(1e-6, 4 * 2.0 ** -24 * zmax))
     check_grad(dx, GradRef(dz, W), f"case {c['i']} dH")
     check_grad(dw, GradRef(dz.T.copy(), X), f"case {c['i']} dW")
+
+
+def _one_pass_cases(count=32, seed=99):
+    rng = np.random.default_rng(seed)
+    out = []
+    for i in range(count):
+        dtype = [torch.float32, torch.bfloat16][int(rng.integers(0, 2))]
+        epv = 4 if dtype == torch.float32 else 8
+        limit = 16 * 1024 * epv  # the kernel's widest row (16 vectors per lane)
+        # vectors per row across the kernels' ranges: up to 4 and 8 per lane
+        # (registers), 9 to 16 per lane (registers and LDS), and their edges
+        nvec = int(rng.choice([1, 3, 64, 1023, 1024, 1025, 4096, 4097, 8191, 8192, 8193,
+                               9000, 12345, 16383, 16384]))
+        v = min(nvec * epv, limit)
+        n = int(rng.choice([1, 2, 7, 300, 1000, 2500]))
+        pad_vecs = int(rng.choice([0, 0, 1, 5]))
+        inplace = bool(rng.integers(0, 2))
+        hint = float(rng.choice([1.0, 0.5, -2.0, 0.0, 3.0e-39, float("inf"), float("nan"), 7.0]))
+        out.append((i, dtype, n, v, pad_vecs * epv, inplace, hint))
+    return out
+
+
+@pytest.mark.parametrize("case", _one_pass_cases(), ids=lambda c: f"case{c[0]}")
+def test_one_pass_sweep(case):
+    """nmce_ce_fwd_bwd through the C ABI on widths across its kernels (up to 4,
+    8 and 16 vectors per lane, the last with part of the row in LDS), padded
+    row strides, in place or into a separate buffer, and hint values that are
+    used as they are or replaced by 1 (zero, subnormal, infinite, NaN). Loss
+    and statistics equal nmce_ce_fwd's bit for bit, the gradient equals
+    nmce_ce_bwd_scaled's for the value the kernel reports it assumed, and an
+    in-place call leaves nothing of the logits but the gradient."""
+    from nmce import _lib as L
+    i, dtype, n, v, pad, inplace, hint = case
+    print(f"[sweep] one-pass case {i}: {dtype} n={n} v={v} pad={pad} inplace={inplace} "
+          f"hint={hint}", flush=True)
+    lib = L.load()
+    assert v <= lib.nmce_ce_fwd_bwd_max_vocab(L.dtype_code(dtype))
+    ld = v + pad
+    g = torch.Generator(device=DEV).manual_seed(40000 + i)
+    slab = torch.zeros((n, ld), dtype=dtype, device=DEV)
+    slab[:, :v] = (torch.randn(n, v, device=DEV, generator=g) * 2.5).to(dtype)
+    t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    t[0] = v - 1
+    if n > 1:
+        t[1] = 0
+    code = L.dtype_code(dtype)
+    stream = L.stream_handle(torch.device(DEV))
+    # two-pass reference: statistics and loss, then the gradient for a value
+    ref = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    L.check(lib.nmce_ce_fwd(slab.data_ptr(), code, n, v, ld, t.data_ptr(), ref[0].data_ptr(),
+                            ref[1].data_ptr(), ref[2].data_ptr(), stream), "fwd")
+    expect = torch.full((1,), hint, dtype=torch.float32, device=DEV)
+    assumed = torch.empty(1, dtype=torch.float32, device=DEV)
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    work = slab.clone()
+    grad = work if inplace else torch.empty((n, v), dtype=dtype, device=DEV)
+    ldg = ld if inplace else v
+    L.check(lib.nmce_ce_fwd_bwd(work.data_ptr(), grad.data_ptr(), code, n, v, ld, ldg,
+                                t.data_ptr(), out[0].data_ptr(), out[1].data_ptr(),
+                                out[2].data_ptr(), expect.data_ptr(), assumed.data_ptr(),
+                                float(n), stream), "fwd_bwd")
+    torch.cuda.synchronize()
+    a = assumed.item()
+    usable = math.isfinite(hint) and abs(hint) >= 1.17549435e-38
+    assert a == (hint if usable else 1.0), (hint, a)
+    bits = torch.int16 if dtype == torch.bfloat16 else torch.int32
+    assert torch.equal(out.view(torch.int32), ref.view(torch.int32)), f"case {i} statistics"
+    want = torch.empty((n, v), dtype=dtype, device=DEV)
+    L.check(lib.nmce_ce_bwd_scaled(slab.data_ptr(), want.data_ptr(), code, n, v, ld, v,
+                                   t.data_ptr(), 0, ref[1].data_ptr(), ref[2].data_ptr(),
+                                   assumed.data_ptr(), 0, float(n), stream), "bwd")
+    torch.cuda.synchronize()
+    got = grad[:, :v] if inplace else grad
+    assert torch.equal(got.view(bits), want.view(bits)), f"case {i} gradient"
+    if inplace and pad:
+        assert torch.equal(work[:, v:], slab[:, v:]), f"case {i} padding touched"
