@@ -52,6 +52,7 @@
 #include <stdint.h>
 
 #include <mutex>
+#include <type_traits>
 
 
 #include "nmce.h"
@@ -285,6 +286,43 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
 // the 32x32 result gives lane l column l%32 and rows 8*(e/4) + 4*(l/32) + e%4.
 __device__ __forceinline__ int acc_row(int fm, int e, int fhalf) {
   return 32 * fm + 8 * (e >> 2) + 4 * fhalf + (e & 3);
+}
+
+// max(a, b, c) as one v_max3_f32 (two IEEE maxNum steps: a quiet NaN operand
+// is ignored). fmaxf gives the same value, but the compiler quiets every
+// operand it cannot prove canonical with a v_max_f32 x, x first, which for
+// MFMA results (never signalling NaNs) only costs issue slots.
+__device__ __forceinline__ float max3_hw(float a, float b, float c) {
+  float r;
+  asm("v_max3_f32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+  return r;
+}
+
+// mask ? a : b, bit by bit, as one v_bfi_b32. Kept opaque: written as a
+// select between two accumulator elements, the compiler turns it into a load
+// at a computed index, which puts the accumulators in scratch memory.
+__device__ __forceinline__ float bit_select(uint32_t mask, float a, float b) {
+  float r;
+  asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mask), "v"(a), "v"(b));
+  return r;
+}
+
+// The element of accumulator fm, column fn, that holds wave row `row` in
+// this lane, when row lies in block fm and row bit 2 is the lane's half (the
+// caller selects among blocks and checks the half): e = 4 * (row bits 3-4) +
+// row bits 0-1. A select tree on the row's bits, 15 v_bfi_b32.
+__device__ __forceinline__ float acc_in_block(const Acc& acc, int fm, int fn, int row) {
+  const uint32_t m0 = 0u - (row & 1), m1 = 0u - ((row >> 1) & 1);
+  const uint32_t m3 = 0u - ((row >> 3) & 1), m4 = 0u - ((row >> 4) & 1);
+  float a[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) a[i] = bit_select(m0, acc.c[fm][fn][2 * i + 1], acc.c[fm][fn][2 * i]);
+  float b[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) b[i] = bit_select(m1, a[2 * i + 1], a[2 * i]);
+  const float c0 = bit_select(m3, b[1], b[0]);
+  const float c1 = bit_select(m3, b[3], b[2]);
+  return bit_select(m4, c1, c0);
 }
 
 // ---------------------------------------------------------------------------
@@ -657,11 +695,17 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
   __syncthreads();  // every wave is done with the operand buffers
   uint32_t* P = reinterpret_cast<uint32_t*>(lds);
   auto pcol = [](int vp, int t) { return t ^ (((vp >> 2) & 15) << 2); };
-#pragma unroll
-  for (int fn = 0; fn < kFN; ++fn) {
+  // One token column (fn) of the wave's 128 rows. This is VALU work with the
+  // MFMA pipe idle, at every tile, so full tiles (all 128 rows of the wave
+  // valid, every token < N: all but the last tile row and column) drop the
+  // per-element row and token masks, take the maximum two values per
+  // v_max3_f32 and find the target's element by a select tree on its row
+  // rather than a compare per element. Both forms give the same bits.
+  auto column = [&](auto full_tag, int fn) {
+    constexpr bool kFull = decltype(full_tag)::value;
     const int tloc = wn * kWaveN + 32 * fn + (lane & 31);
     const int64_t tok = n0 + tloc;
-    const bool tok_ok = tok < N;
+    const bool tok_ok = kFull || tok < N;
     int tl = -1;  // target row within this wave's valid rows, or -1
     if (tok_ok) {
       const int64_t t = target[tok] - vstart - vrow0;
@@ -669,15 +713,32 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
     }
     float mx = kMaxFloorL;
     float pick = 0.0f;
+    if constexpr (kFull) {
+      float m4[kFM], z4[kFM];
 #pragma unroll
-    for (int fm = 0; fm < kFM; ++fm)
+      for (int fm = 0; fm < kFM; ++fm) {
+        m4[fm] = kMaxFloorL;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int r = acc_row(fm, e, fhalf);
-        const float z = acc.c[fm][fn][e];
-        if (r < valid_rows) mx = fmaxf(mx, z);
-        pick = (r == tl) ? z : pick;
+        for (int e = 0; e < 16; e += 2)
+          m4[fm] = max3_hw(m4[fm], acc.c[fm][fn][e], acc.c[fm][fn][e + 1]);
+        z4[fm] = acc_in_block(acc, fm, fn, tl);
       }
+      mx = max3_hw(m4[0], m4[1], max3_hw(m4[2], m4[3], kMaxFloorL));
+      const float za = (tl & 32) ? z4[1] : z4[0];
+      const float zb = (tl & 32) ? z4[3] : z4[2];
+      const float z = (tl & 64) ? zb : za;
+      pick = (tl >= 0 && ((tl >> 2) & 1) == fhalf) ? z : 0.0f;
+    } else {
+#pragma unroll
+      for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = acc_row(fm, e, fhalf);
+          const float z = acc.c[fm][fn][e];
+          if (r < valid_rows) mx = fmaxf(mx, z);
+          pick = (r == tl) ? z : pick;
+        }
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     // sum exp(z - mx) - 1 with the terms equal to 1 counted apart (as in
     // lmhead_stats_kernel); each exponential also goes to the LDS tile.
@@ -688,7 +749,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int r = acc_row(fm, e, fhalf);
-        const float p = r < valid_rows ? exp_shift(acc.c[fm][fn][e], mx) : 0.0f;
+        const float p = (kFull || r < valid_rows) ? exp_shift(acc.c[fm][fn][e], mx) : 0.0f;
         se += p;
         sr += __builtin_amdgcn_fractf(p);
         d[e] = tok_ok ? p : 0.0f;
@@ -709,6 +770,21 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
       pmax[blk * N + tok] = mx;
       psum1[blk * N + tok] = (ones - 1.0f) + sr;
       ptgt[blk * N + tok] = pick;
+    }
+  };
+  // One column at a time: both at once would need every accumulator in
+  // VGPRs together and spill.
+  if (valid_rows == kWaveM && n0 + kBN <= N) {
+#pragma unroll
+    for (int fn = 0; fn < kFN; ++fn) {
+      column(std::true_type{}, fn);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+#pragma unroll
+    for (int fn = 0; fn < kFN; ++fn) {
+      column(std::false_type{}, fn);
+      __builtin_amdgcn_sched_barrier(0);
     }
   }
   __syncthreads();
