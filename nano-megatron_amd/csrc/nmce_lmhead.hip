@@ -818,12 +818,13 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
 // and, on the target row, (softmax - 1) * g from the fp32 target logit
 // (target_grad). Written in place into pt (vocabulary-major, the dW GEMM's A)
 // and transposed into dz [N, ldz] (token-major, the dX GEMM's A). A workgroup
-// takes one 128-row block of partial statistics and 128 tokens; the factor of
+// takes one 128-row block of partial statistics and 256 tokens; the factor of
 // each (block, token) is formed once. Rows past V and blocks past nb come out
 // 0 (pt holds 0 there), tokens past N are not written to dz.
 // ---------------------------------------------------------------------------
 constexpr int kRsRows = kPartialRows;  // 128: one block of partial statistics
-constexpr int kRsToks = 128;
+constexpr int kRsToks = 256;
+constexpr int kRsLdsBytes = kRsToks * (kRsRows / 2) * 4;  // the tile, 64 KiB
 __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
     uint16_t* __restrict__ pt, int64_t ldt, uint16_t* __restrict__ dz, int64_t ldz, int64_t V,
     int64_t N, const float* __restrict__ pmax, int64_t nb, const float* __restrict__ gmax,
@@ -833,11 +834,12 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
   __shared__ float s_scale[kRsToks];
   __shared__ float s_dt[kRsToks];
   __shared__ int s_tv[kRsToks];
-  // The tile, token-major, as words of two vocabulary rows: word q of token
-  // t holds rows 2q (low half) and 2q + 1 (high half), at t * 64 +
-  // (q ^ 4 ((t >> 3) & 15)). The XOR spreads both the word writes of the pt
-  // pass and the 16-byte reads of the dz pass over all 64 banks.
-  __shared__ __align__(16) uint32_t tile[kRsToks * (kRsRows / 2)];
+  // The tile (dynamic LDS, kRsLdsBytes), token-major, as words of two
+  // vocabulary rows: word q of token t holds rows 2q (low half) and 2q + 1
+  // (high half), at t * 64 + (q ^ 4 ((t >> 3) & 15)). The XOR spreads the
+  // 16-byte reads of the dz pass over all 64 banks, and the word writes of
+  // the pt pass over 32 of them (two-way conflicts).
+  extern __shared__ __align__(16) uint32_t tile[];
   const int64_t blk = blockIdx.x;
   const int64_t v0 = blk * kRsRows;
   const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kRsToks;
@@ -864,9 +866,10 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
   const int lane = tid & 63;
   const int wave = tid >> 6;
   // pt pass: a lane takes tokens 8s .. 8s + 7 of two adjacent rows per
-  // iteration; a wave's load covers four rows' 256-byte segments. The last
-  // tile of a row may stop at ldt (a multiple of 64) halfway.
-  const int sg = lane & 15;
+  // iteration; a wave's load covers two rows' 512-byte segments (256-byte
+  // ones ran 1% slower over the step). The last tile of a row may stop at ldt
+  // (a multiple of 64) partway.
+  const int sg = lane & 31;
   const int tg = 8 * sg;
   const bool tok_ok = t0 + tg < ldt;
   auto fix = [&](float* f, int r) {
@@ -881,8 +884,8 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
     }
   };
 #pragma unroll
-  for (int it = 0; it < kRsRows / 2 / 16; ++it) {
-    const int q = (lane >> 4) + 4 * (wave + 4 * it);  // row pair
+  for (int it = 0; it < kRsRows / 2 / 8; ++it) {
+    const int q = (lane >> 5) + 2 * (wave + 4 * it);  // row pair
     const int r = 2 * q;
     u32x4* p0 = reinterpret_cast<u32x4*>(pt + (v0 + r) * ldt + t0 + tg);
     u32x4* p1 = reinterpret_cast<u32x4*>(pt + (v0 + r + 1) * ldt + t0 + tg);
@@ -1008,6 +1011,10 @@ int configure_lds() {
         hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return static_cast<int>(e);
   }
+  const hipError_t e =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&lmhead_dz_rescale_kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, kRsLdsBytes);
+  if (e != hipSuccess) return static_cast<int>(e);
   lds_configured = true;
   return NMCE_OK;
 }
@@ -1512,7 +1519,7 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
   hipLaunchKernelGGL(lmhead_dz_rescale_kernel,
                      dim3(static_cast<unsigned>(L.vpad / kRsRows),
                           static_cast<unsigned>((L.ldt + kRsToks - 1) / kRsToks)),
-                     dim3(256), 0, s, pt, L.ldt, dz, L.vpad, V, nc, pmax, L.nb, g_max + t0,
+                     dim3(256), kRsLdsBytes, s, pt, L.ldt, dz, L.vpad, V, nc, pmax, L.nb, g_max + t0,
                      g_sumexp_m1 + t0, target_logit + t0, target + t0, vocab_start,
                      grad_output + t0 * gout_stride, gout_stride, gout_div);
   if ((st = launch_status())) return st;
