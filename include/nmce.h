@@ -115,6 +115,9 @@ int nmce_ce_combine(const float* row_max, const float* row_sumexp_m1,
  * [0, vocab_total)). Writes nmce_validate_slots(n_rows) int32 counts of bad
  * targets, one per NMCE_VALIDATE_ROWS_PER_SLOT rows; every slot is written,
  * so the buffer needs no clearing. The caller raises if any count is nonzero.
+ * bad_counts may be device memory or pinned host memory (hipHostMalloc,
+ * which the device addresses at its host address): the Python host writes
+ * the counts straight to the host that way, with no copy after the kernel.
  */
 int64_t nmce_validate_slots(int64_t n_rows);
 int nmce_validate_targets(const int64_t* target, int64_t n_rows,

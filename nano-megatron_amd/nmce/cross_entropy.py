@@ -147,22 +147,31 @@ _CHECK_POLLS = 200
 
 
 class _PendingCheck:
-    """Bad-target counts on their way to pinned host memory."""
+    """Bad-target counts on their way to pinned host memory.
+
+    The check kernel writes the counts straight into ``host`` (pinned memory
+    is mapped into the device's address space at its host address), so the
+    buffer must stay alive until ``event`` has completed: every caller ends
+    with ``raise_if_bad()`` or, when it leaves early on an exception,
+    ``wait()``.
+    """
 
     def __init__(self, host: torch.Tensor, event: torch.cuda.Event):
         self.host = host
         self.event = event
 
-    def raise_if_bad(self) -> None:
+    def wait(self) -> None:
         # The counts usually reach the host within microseconds of the call:
         # poll first, so that a blocking wait's wake-up latency (tens of
         # microseconds, per step of a small batch) is paid only by long waits.
         event = self.event
         for _ in range(_CHECK_POLLS):
             if event.query():
-                break
-        else:
-            event.synchronize()
+                return
+        event.synchronize()
+
+    def raise_if_bad(self) -> None:
+        self.wait()
         if int(self.host.sum()) != 0:
             raise ValueError("target token id is outside the model vocabulary")
 
@@ -184,11 +193,11 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
                         on_side_stream: bool = True) -> _PendingCheck | None:
     """Start the target check of cross_entropy.py:79-81 without blocking.
 
-    One kernel counts targets outside ``[0, vocab_size)`` and the counts are
-    copied into pinned host memory, both on a side stream ordered after the
-    work already queued on the current stream; ``raise_if_bad()`` on the
-    result waits for that copy alone. The loss kernels go on the current
-    stream meanwhile, so the check adds nothing to the loss stream's timeline.
+    One kernel counts targets outside ``[0, vocab_size)`` straight into pinned
+    host memory, on a side stream ordered after the work already queued on the
+    current stream; ``raise_if_bad()`` on the result waits for that kernel
+    alone. The loss kernels go on the current stream meanwhile, so the check
+    adds nothing to the loss stream's timeline.
     """
     lib = _lib.load()
     t = target.reshape(-1)
@@ -198,15 +207,13 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
     if n == 0:
         return None
     slots = lib.nmce_validate_slots(n)
+    host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
     if not on_side_stream:
         # On the loss stream, ahead of a kernel that fills every compute unit
         # for its whole run (the one-pass forward), so that the host's wait
         # ends early instead of after that kernel.
-        counts = torch.empty(slots, dtype=torch.int32, device=t.device)
         _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
-                vocab_size, counts.data_ptr(), _lib.stream_handle(t.device))
-        host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
-        host.copy_(counts, non_blocking=True)
+                vocab_size, host.data_ptr(), _lib.stream_handle(t.device))
         event = torch.cuda.Event()
         if t.device.index is None or t.device.index == torch.cuda.current_device():
             event.record()  # the current device's current stream
@@ -217,11 +224,8 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
     side = _side_stream(t.device)
     side.wait_stream(main)  # the targets are complete in the current stream's order
     with torch.cuda.stream(side):
-        counts = torch.empty(slots, dtype=torch.int32, device=t.device)
         _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
-                vocab_size, counts.data_ptr(), side.cuda_stream)
-        host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
-        host.copy_(counts, non_blocking=True)
+                vocab_size, host.data_ptr(), side.cuda_stream)
         event = torch.cuda.Event()
         event.record(side)
     t.record_stream(side)  # keep the targets' memory until the side stream is done
@@ -583,8 +587,13 @@ def vocab_parallel_cross_entropy(
     # The loss kernels are enqueued before the host waits for the check, so
     # the GPU is busy while the host reads the counts. They never read out of
     # bounds on a bad target; their result is discarded when the check fails.
-    loss = _VocabParallelCrossEntropyMean.apply(
-        logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, hint)
+    try:
+        loss = _VocabParallelCrossEntropyMean.apply(
+            logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, hint)
+    except BaseException:
+        if pending is not None:
+            pending.wait()
+        raise
     if pending is not None:
         pending.raise_if_bad()
     return loss

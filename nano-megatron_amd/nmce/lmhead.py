@@ -472,7 +472,6 @@ def lmhead_vocab_parallel_cross_entropy(
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
     _check_target(target, hidden.shape[:-1], hidden.device)
     want_grad = torch.is_grad_enabled() and (hidden.requires_grad or weight.requires_grad)
-    pending = launch_target_check(target, vocab_size) if validate else None
     if one_pass and want_grad:
         if upstream_hint is None:
             caller = sys._getframe(1)
@@ -480,13 +479,20 @@ def lmhead_vocab_parallel_cross_entropy(
         else:
             _check_hint(upstream_hint, hidden.device)
             hint = upstream_hint
-        loss = _LMHeadVocabParallelCrossEntropyMean.apply(
-            hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, hint,
-            token_chunk)
-    else:
-        loss = _LMHeadVocabParallelCrossEntropy.apply(
-            hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size,
-            vocab_chunk).mean()
+    pending = launch_target_check(target, vocab_size) if validate else None
+    try:
+        if one_pass and want_grad:
+            loss = _LMHeadVocabParallelCrossEntropyMean.apply(
+                hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, hint,
+                token_chunk)
+        else:
+            loss = _LMHeadVocabParallelCrossEntropy.apply(
+                hidden, weight, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size,
+                vocab_chunk).mean()
+    except BaseException:
+        if pending is not None:
+            pending.wait()  # the check kernel writes into the pending host buffer
+        raise
     if pending is not None:
         pending.raise_if_bad()
     return loss

@@ -394,6 +394,49 @@ def test_out_of_vocabulary_target_raises():
     nmce.validate_targets(t, ctx.tp_size * 16)
 
 
+def test_target_check_waits_when_the_loss_raises(monkeypatch):
+    """The check kernel writes its counts straight into a pinned host buffer,
+    so a loss call that leaves on an exception must still wait for it before
+    the buffer can go back to the allocator; both wrappers do."""
+    import nmce
+    from nmce import cross_entropy as ce
+    from nmce import lmhead as lm
+    waited = []
+    real_wait = ce._PendingCheck.wait
+
+    def wait(self):
+        waited.append(self)
+        real_wait(self)
+
+    monkeypatch.setattr(ce._PendingCheck, "wait", wait)
+
+    def boom(*args, **kwargs):
+        raise RuntimeError("planted")
+
+    ctx = nmce.ParallelContext.single()
+    t = torch.zeros(2, 3, dtype=torch.long, device=DEV)
+    for one_pass in (True, False):
+        x = torch.randn(2, 3, 16, device=DEV, requires_grad=True)
+        monkeypatch.setattr(ce._VocabParallelCrossEntropyMean, "apply", boom)
+        with pytest.raises(RuntimeError, match="planted"):
+            nmce.vocab_parallel_cross_entropy(x * 1.0, t, 0, 16, ctx, one_pass=one_pass)
+        monkeypatch.undo()
+        monkeypatch.setattr(ce._PendingCheck, "wait", wait)
+    h = torch.randn(6, 64, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    w = torch.randn(16, 64, device=DEV).to(torch.bfloat16).requires_grad_(True)
+    monkeypatch.setattr(lm._LMHeadVocabParallelCrossEntropyMean, "apply", boom)
+    with pytest.raises(RuntimeError, match="planted"):
+        nmce.lmhead_vocab_parallel_cross_entropy(h, w, t.reshape(-1), 0, 16, ctx)
+    assert len(waited) == 3
+    assert all(p.event.query() for p in waited)
+    # and the normal path still raises on a bad target after the direct write
+    monkeypatch.undo()
+    bad = t.clone()
+    bad[0, 1] = 16
+    with pytest.raises(ValueError, match="target token id is outside the model vocabulary"):
+        nmce.vocab_parallel_cross_entropy(torch.randn(2, 3, 16, device=DEV), bad, 0, 16, ctx)
+
+
 def test_bf16_dropin_returns_bf16_grad_and_fp32_loss():
     """bf16 logits -> fp32 loss (test_recompute.py:72-75), bf16 grad."""
     import nmce
