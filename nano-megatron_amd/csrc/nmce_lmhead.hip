@@ -91,11 +91,13 @@ constexpr int kBlocksA = kBM / 8;
 constexpr int kBlocksB = kBN / 8;
 constexpr int kBlocksPerWave = (kBlocksA + kBlocksB) / (kWavesM * kWavesN);
 static_assert(kBlocksA % kBlocksPerWave == 0, "a wave loads blocks of one operand only");
-// Tile rows per raster group inside an XCD band. The forward walks the whole
-// weight shard (hundreds of tile rows) and runs faster with groups of 4; the
-// chunked recomputation and the plain GEMM with groups of 8 (measured).
+// Tile rows per raster group inside an XCD band (measured): groups of 4 for
+// the forward, which walks the whole weight shard (hundreds of tile rows),
+// and for the one-pass backward products (dX 1%, dW 1.5-2% faster than with
+// 8); groups of 8 for the chunked recomputation and the plain GEMM.
 constexpr int kGroupM = 8;
 constexpr int kGroupMStats = 4;
+constexpr int kGroupMProducts = 4;
 constexpr int kXcds = 8;
 constexpr float kMaxFloorL = -1.0e38f;
 
@@ -111,19 +113,19 @@ __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" 
 
 // Tile index for this workgroup. The dispatcher deals workgroups to the 8 XCDs
 // round-robin (block b runs on XCD b % 8); give each XCD a contiguous band of
-// tile ids, and inside the band walk groups of kGM tile rows column by
+// tile ids, and inside the band walk groups of group_m tile rows column by
 // column, so the tiles that run together on one L2 share A and B stripes.
-template <int kGM>
-__device__ __forceinline__ void tile_coords(int tiles_m, int tiles_n, int& tm, int& tn) {
+__device__ __forceinline__ void tile_coords(int group_m, int tiles_m, int tiles_n, int& tm,
+                                            int& tn) {
   const int total = tiles_m * tiles_n;
   const int b = blockIdx.x;
   const int xcd = b % kXcds;
   const int q = total / kXcds, r = total % kXcds;
   const int tid = xcd * q + (xcd < r ? xcd : r) + b / kXcds;
-  const int group = kGM * tiles_n;
+  const int group = group_m * tiles_n;
   const int g = tid / group;
-  const int first_m = g * kGM;
-  const int gm = (tiles_m - first_m) < kGM ? (tiles_m - first_m) : kGM;
+  const int first_m = g * group_m;
+  const int gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
   const int in_g = tid - g * group;
   tm = first_m + in_g % gm;
   tn = in_g / gm;
@@ -339,7 +341,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
   const int tiles_m = static_cast<int>((V + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
   int tm, tn;
-  tile_coords<kGroupMStats>(tiles_m, tiles_n, tm, tn);
+  tile_coords(kGroupMStats, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
   gemm_mainloop(W, H, V, X, H, N, H, m0, n0, lds, acc);
@@ -458,7 +460,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   const int tiles_m = static_cast<int>(Mpad / kBM);
   const int tiles_n = static_cast<int>((ldt + kBN - 1) / kBN);
   int tm, tn;
-  tile_coords<kGroupM>(tiles_m, tiles_n, tm, tn);
+  tile_coords(kGroupM, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
   gemm_mainloop(Wc, H, Mvalid, X, H, N, H, m0, n0, lds, acc);
@@ -571,12 +573,12 @@ template <int kMode>
 __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
     const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
     int64_t ldb, int64_t N, int64_t K, uint16_t* __restrict__ C, float* __restrict__ Cf,
-    int64_t ldc) {
+    int64_t ldc, int group_m) {
   extern __shared__ __align__(16) char lds[];
   const int tiles_m = static_cast<int>((M + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
   int tm, tn;
-  tile_coords<kGroupM>(tiles_m, tiles_n, tm, tn);
+  tile_coords(group_m, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
   gemm_mainloop(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
@@ -678,7 +680,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
   const int tiles_m = static_cast<int>((V + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
   int tm, tn;
-  tile_coords<kGroupMStats>(tiles_m, tiles_n, tm, tn);
+  tile_coords(kGroupMStats, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
   gemm_mainloop(W, H, V, X, H, N, H, m0, n0, lds, acc);
@@ -1027,14 +1029,14 @@ inline bool operand_ok(const void* p, int64_t ld) {
 
 int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const uint16_t* B,
                       int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf, int64_t ldc,
-                      hipStream_t stream) {
+                      hipStream_t stream, int group_m = kGroupM) {
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   const dim3 grid(static_cast<unsigned>(tiles));
   switch (mode) {
-    case 0: hipLaunchKernelGGL(gemm_store_kernel<0>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
-    case 1: hipLaunchKernelGGL(gemm_store_kernel<1>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
-    case 2: hipLaunchKernelGGL(gemm_store_kernel<2>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
-    default: hipLaunchKernelGGL(gemm_store_kernel<3>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc); break;
+    case 0: hipLaunchKernelGGL(gemm_store_kernel<0>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
+    case 1: hipLaunchKernelGGL(gemm_store_kernel<1>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
+    case 2: hipLaunchKernelGGL(gemm_store_kernel<2>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
+    default: hipLaunchKernelGGL(gemm_store_kernel<3>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
   }
   return launch_status();
 }
@@ -1528,7 +1530,8 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
   // dX rows of the chunk = dZ_c W (K = the padded vocabulary; the padding of
   // dz and W^T is zero).
   if ((st = launch_gemm_store(0, dz, L.vpad, nc, wt, L.vpad, H, L.vpad,
-                              static_cast<uint16_t*>(grad_hidden) + t0 * H, nullptr, H, s)))
+                              static_cast<uint16_t*>(grad_hidden) + t0 * H, nullptr, H, s,
+                              kGroupMProducts)))
     return st;
   // dW (+)= dZ_c^T X_c (K = the chunk's padded tokens), accumulated in fp32
   // across chunks and rounded to bf16 by the last.
@@ -1539,7 +1542,7 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
   else mode = 3;
   return launch_gemm_store(mode, pt, L.ldt, V, xt, L.ldt, H, L.ldt,
                            static_cast<uint16_t*>(grad_weight),
-                           reinterpret_cast<float*>(ws + L.off_acc), H, s);
+                           reinterpret_cast<float*>(ws + L.off_acc), H, s, kGroupMProducts);
 }
 
 }  // extern "C"
