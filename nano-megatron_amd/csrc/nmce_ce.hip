@@ -695,13 +695,8 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
 // scaled by gout[0] / assumed[0] (each is linear in the upstream value:
 // cross_entropy.py:64). Rows as in the one-pass kernel (16-byte aligned, V a
 // whole number of vectors), walked on its grid, so that a hit costs one short
-// launch: 256-lane workgroups (a quarter of the waves of the row backward's,
-// each with twice the loads in flight on a miss), since launching the waves
-// is most of a hit's time. gout[0] also goes to observed[0] for the next
-// forward.
-constexpr int kRescaleBlock = 256;
-constexpr int kRescaleUnroll = 8;
-template <typename T, int kBlock = kRescaleBlock, int kUnroll = kRescaleUnroll>
+// launch. gout[0] also goes to observed[0] for the next forward.
+template <typename T, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
 __global__ __launch_bounds__(kBlock) void ce_grad_rescale_kernel(
     T* g, int64_t n_rows, int64_t V, int64_t ldg, const float* __restrict__ gout,
     const float* __restrict__ assumed, float* __restrict__ observed) {
@@ -1095,7 +1090,7 @@ int nmce_ce_grad_rescale_unless(void* grad, int dtype, int64_t n_rows, int64_t v
   if (!grad || !grad_output || !assumed) return NMCE_EINVAL_PTR;
   if (reinterpret_cast<uintptr_t>(grad) % 16 || (ld_grad * es) % 16) return NMCE_EINVAL_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(one_pass_grid(n_rows)), block(kRescaleBlock);
+  const dim3 grid(one_pass_grid(n_rows)), block(kBwdBlock);
   if (dtype == NMCE_F32)
     hipLaunchKernelGGL(ce_grad_rescale_kernel<float>, grid, block, 0, st,
                        static_cast<float*>(grad), n_rows, vocab, ld_grad, grad_output, assumed,
