@@ -716,20 +716,26 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
     float mx = kMaxFloorL;
     float pick = 0.0f;
     if constexpr (kFull) {
-      float m4[kFM], z4[kFM];
+      float m4[kFM];
 #pragma unroll
       for (int fm = 0; fm < kFM; ++fm) {
         m4[fm] = kMaxFloorL;
 #pragma unroll
         for (int e = 0; e < 16; e += 2)
           m4[fm] = max3_hw(m4[fm], acc.c[fm][fn][e], acc.c[fm][fn][e + 1]);
-        z4[fm] = acc_in_block(acc, fm, fn, tl);
       }
       mx = max3_hw(m4[0], m4[1], max3_hw(m4[2], m4[3], kMaxFloorL));
-      const float za = (tl & 32) ? z4[1] : z4[0];
-      const float zb = (tl & 32) ? z4[3] : z4[2];
-      const float z = (tl & 64) ? zb : za;
-      pick = (tl >= 0 && ((tl >> 2) & 1) == fhalf) ? z : 0.0f;
+      // A wave's 64 tokens of this column have a target among its 128 rows
+      // only about once in 16 (128 of V rows): skip the tree otherwise.
+      if (__builtin_amdgcn_ballot_w64(tl >= 0)) {
+        float z4[kFM];
+#pragma unroll
+        for (int fm = 0; fm < kFM; ++fm) z4[fm] = acc_in_block(acc, fm, fn, tl);
+        const float za = (tl & 32) ? z4[1] : z4[0];
+        const float zb = (tl & 32) ? z4[3] : z4[2];
+        const float z = (tl & 64) ? zb : za;
+        pick = (tl >= 0 && ((tl >> 2) & 1) == fhalf) ? z : 0.0f;
+      }
     } else {
 #pragma unroll
       for (int fm = 0; fm < kFM; ++fm)
