@@ -290,6 +290,17 @@ __device__ __forceinline__ int acc_row(int fm, int e, int fhalf) {
   return 32 * fm + 8 * (e >> 2) + 4 * fhalf + (e & 3);
 }
 
+// The epilogues stage a 256 x 256 bf16 tile in LDS as words of two rows: word
+// (vp, c) at vp * kBN + (c ^ 4 ((vp >> 2) & 15)) holds rows 2 vp and 2 vp + 1
+// of column c. Accumulator fm, element group q (elements 4q .. 4q + 3) of a
+// lane covers row pairs vp and vp + 1 with vp = wm * 64 + 16 fm + 4 q +
+// 2 fhalf, so vp >> 2 = 16 wm + 4 fm + q and the swizzle is a constant per
+// (fm, q): from the lane's base P + (wm * 64 + 2 fhalf) * kBN, the word of
+// column c is at a constant row offset and c XOR a constant.
+__device__ __forceinline__ uint32_t* stage_word(uint32_t* lane_base, int fm, int q, int c) {
+  return lane_base + (16 * fm + 4 * q) * kBN + (c ^ (((4 * fm + q) & 15) << 2));
+}
+
 // max(a, b, c) as one v_max3_f32 (two IEEE maxNum steps: a quiet NaN operand
 // is ignored). fmaxf gives the same value, but the compiler quiets every
 // operand it cannot prove canonical with a v_max_f32 x, x first, which for
@@ -520,11 +531,9 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
       // word P[v/2][t] = bf16(d[v]) | bf16(d[v+1]) << 16, tile-local v and t.
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int vp = (wm * kWaveM + 32 * fm + 8 * q + 4 * fhalf) >> 1;
-        // vp is even, so vp and vp + 1 share a block of 4 and a swizzle
-        const int col = pcol(vp, tloc);
-        P[vp * kBN + col] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
-        P[(vp + 1) * kBN + col] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
+        uint32_t* w = stage_word(P + (wm * kWaveM / 2 + 2 * fhalf) * kBN, fm, q, tloc);
+        w[0] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
+        w[kBN] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
       }
     }
   }
@@ -604,11 +613,9 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
       for (int fm = 0; fm < kFM; ++fm)
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
-          const int vp = (wm * kWaveM + 32 * fm + 8 * q + 4 * fhalf) >> 1;
-          const int col = pcol(vp, cloc);
-          P[vp * kBN + col] = pack_bf16x2(acc.c[fm][fn][4 * q], acc.c[fm][fn][4 * q + 1]);
-          P[(vp + 1) * kBN + col] =
-              pack_bf16x2(acc.c[fm][fn][4 * q + 2], acc.c[fm][fn][4 * q + 3]);
+          uint32_t* w = stage_word(P + (wm * kWaveM / 2 + 2 * fhalf) * kBN, fm, q, cloc);
+          w[0] = pack_bf16x2(acc.c[fm][fn][4 * q], acc.c[fm][fn][4 * q + 1]);
+          w[kBN] = pack_bf16x2(acc.c[fm][fn][4 * q + 2], acc.c[fm][fn][4 * q + 3]);
         }
     }
     __syncthreads();
@@ -764,10 +771,9 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
       }
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        const int vp = (wm * kWaveM + 32 * fm + 8 * q + 4 * fhalf) >> 1;
-        const int col = pcol(vp, tloc);
-        P[vp * kBN + col] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
-        P[(vp + 1) * kBN + col] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
+        uint32_t* w = stage_word(P + (wm * kWaveM / 2 + 2 * fhalf) * kBN, fm, q, tloc);
+        w[0] = pack_bf16x2(d[4 * q], d[4 * q + 1]);
+        w[kBN] = pack_bf16x2(d[4 * q + 2], d[4 * q + 3]);
       }
     }
     se += __shfl_xor(se, 32);
