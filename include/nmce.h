@@ -351,10 +351,12 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
  * all at once). Per chunk the statistics GEMM keeps its exponentials
  * P = exp(z - block max) in the workspace; once the chunk's statistics are
  * combined across the TP group, dZ follows from P by one factor per
- * (128-row block, token), and the dX rows of the chunk and its share of dW
- * are formed by libnmce's GEMM. Nothing of size [n_rows, vocab_local] exists
- * (a chunk's P and dZ are [token_chunk, vocab_local]), and the logits are
- * computed once: 6 * n_rows * vocab_local * hidden_size flops in all.
+ * (128-row block, token), in place, and the dX rows of the chunk and its
+ * share of dW are formed by libnmce's GEMM, which reads dZ^T, the weight and
+ * the hidden rows as they lie (no transposed copies). Nothing of size
+ * [n_rows, vocab_local] exists (a chunk's P, then dZ^T, is [vocab_local,
+ * token_chunk]), and the logits are computed once: 6 * n_rows * vocab_local
+ * * hidden_size flops in all.
  * Replaces model.py:192 followed by cross_entropy.py:17-65 and the matmul
  * backward of model.py:192; with a caller that assumes the right upstream
  * value, as the reference's forward computes the softmax its backward
@@ -362,14 +364,15 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
  * --------------------------------------------------------------------------- */
 
 /*
- * Workspace layout (int64 values) written to layout[0 .. 11]:
+ * Workspace layout (int64 values) written to layout[0 .. 8]:
  *   [0] total bytes  [1] chunk (tokens per chunk)  [2] n_chunks
  *   [3] ldt (chunk padded to 64)  [4] vpad (vocab_local padded to 256)
- *   [5] nb (ceil(vocab_local / 128))  [6..11] byte offsets of W^T, X_c^T,
- *   P^T (= dZ_c^T), dZ_c, the partial statistics and the fp32 dW
- *   accumulator (present when n_chunks > 1).
+ *   [5] nb (ceil(vocab_local / 128))  [6..8] byte offsets of P^T
+ *   (= dZ_c^T, [vpad, ldt]: the only chunk-sized buffer; both backward
+ *   products read it, hidden and weight as they lie), the partial statistics
+ *   and the fp32 dW accumulator (present when n_chunks > 1).
  */
-#define NMCE_LMHEAD_FUSED_LAYOUT_FIELDS 12
+#define NMCE_LMHEAD_FUSED_LAYOUT_FIELDS 9
 int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
                                 int64_t token_chunk, int64_t* layout);
 
@@ -377,12 +380,6 @@ int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t voc
  * NaN (a gradient written for such a value could not be rescaled). Both are
  * device pointers to one float. */
 int nmce_hint_assume(const float* hint, float* assumed, void* stream);
-
-/* Once per forward, before the chunks: W^T into the workspace. */
-int nmce_lmhead_ce_fused_prepare(const void* hidden, const void* weight, int dtype,
-                                 int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
-                                 int64_t token_chunk, void* workspace, int64_t workspace_bytes,
-                                 void* stream);
 
 /*
  * Chunk c (tokens [c*chunk, min((c+1)*chunk, n_rows))): this shard's
@@ -430,6 +427,17 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
  */
 int nmce_gemm_nt_bf16(const void* a, int64_t lda, const void* b, int64_t ldb, int64_t m,
                       int64_t n, int64_t k, void* c, int c_dtype, int64_t ldc, void* stream);
+
+/*
+ * The same core with b MN-contiguous, as the fused backward products read
+ * their operands (no counterpart in the reference; for tests):
+ * c[i, j] = sum_l a(i, l) * b[l, j] with b [k, ldb], and a[i, l] ([m, lda],
+ * K-contiguous) or, when a_mn, a[l, i] ([k, lda], MN-contiguous); bf16 c.
+ * MN-contiguous operands need ld >= (columns rounded up to 8), 64 * ld < 2^31.
+ * Bit-identical to nmce_gemm_nt_bf16 on the transposed operands.
+ */
+int nmce_gemm_mn_bf16(int a_mn, const void* a, int64_t lda, const void* b, int64_t ldb,
+                      int64_t m, int64_t n, int64_t k, void* c, int64_t ldc, void* stream);
 
 #ifdef __cplusplus
 }

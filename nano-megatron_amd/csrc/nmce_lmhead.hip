@@ -5,8 +5,9 @@
 // nano_megatron/cross_entropy.py:16-65, without ever holding Z for the whole
 // vocabulary.
 //
-// Every product is one bf16 "NT" GEMM shape, C[m, n] = sum_k A[m, k] * B[n, k]
-// with both operands K-contiguous, on v_mfma_f32_32x32x16_bf16:
+// Every product is one bf16 GEMM core, C[m, n] = sum_k A[m, k] * B[n, k] on
+// v_mfma_f32_32x32x16_bf16, each operand K-contiguous or MN-contiguous
+// (gemm_mainloop):
 //
 //   forward   Z^T = W X^T    (M = vocab, N = tokens, K = hidden). The epilogue
 //             reduces each 128-row vocabulary block of a token's column to a
@@ -18,14 +19,17 @@
 //             dX    += dZ_c W_c      (M = tokens, N = hidden, K = Vc; B = W^T)
 //
 // The one-pass path (the drop-in's default) computes Z once, per chunk of
-// tokens (all of them when the chunk's buffers fit the caller's budget):
+// tokens (all of them when the chunk's buffer fits the caller's budget):
 //             P^T  = exp(W X^T - block max), bf16, with the partial statistics
-//             dZ^T = P^T * exp(block max - M) * g / S - onehot, in place, and
-//                    its transpose dZ (once the statistics are combined)
-//             dX   = dZ W            (via W^T, K = vocab)
-//             dW  += dZ^T X          (via X^T, K = the chunk's tokens; fp32
-//                                     across chunks only when there are several)
-// so 6 N V H flops in all, against 8 N V H for the recomputing backward.
+//             dZ^T = P^T * exp(block max - M) * g / S - onehot, in place
+//                    (once the statistics are combined)
+//             dX   = dZ W            (K = vocab; dZ^T and W both read
+//                                     vocabulary-row major, as they lie)
+//             dW  += dZ^T X          (K = the chunk's tokens; X read token-row
+//                                     major, as it lies; fp32 across chunks
+//                                     only when there are several)
+// so 6 N V H flops in all, against 8 N V H for the recomputing backward, and
+// no transposed copy of any operand.
 //
 // Tokens are the MFMA N dimension in the loss GEMMs: the 32x32 accumulator
 // gives each lane 16 vocabulary rows of a single token, so the per-token
@@ -37,13 +41,17 @@
 // Each wave reads its next fragments from LDS under the MFMAs of the current
 // ones (two register sets, one LDS read pinned after each MFMA). Operand tiles
 // move HBM/L2 -> LDS with 16-byte direct-to-LDS loads (MUBUF
-// buffer_load_dwordx4 ... lds, no VGPR staging), double-buffered, rows of 128
-// bytes with the 16-byte chunks XOR-swizzled by ((row >> 1) & 7). gfx950's LDS
-// has 64 banks, so a ds_read_b128 serves 16 lanes (16 consecutive rows of a
-// fragment) per cycle; this swizzle puts those 16 rows on 16 distinct 16-byte
-// bank groups (row parity picks the half of the banks, the swizzled chunk the
-// group). Workgroups are mapped to tiles so that each XCD (one L2) owns a
-// contiguous band of tiles walked in groups that share operands.
+// buffer_load_dwordx4 ... lds, no VGPR staging), double-buffered. A
+// K-contiguous operand sits in rows of 128 bytes with the 16-byte chunks
+// XOR-swizzled by ((row >> 1) & 7). gfx950's LDS has 64 banks, so a
+// ds_read_b128 serves 16 lanes (16 consecutive rows of a fragment) per cycle;
+// this swizzle puts those 16 rows on 16 distinct 16-byte bank groups (row
+// parity picks the half of the banks, the swizzled chunk the group). An
+// MN-contiguous operand sits in 64 k-rows of 512 bytes and its fragments come
+// from gfx950's transposing LDS read, ds_read_b64_tr_b16, with the same
+// fragments, so the two layouts give the same bits. Workgroups are mapped to
+// tiles so that each XCD (one L2) owns a contiguous band of tiles walked in
+// groups that share operands.
 //
 // The dZ epilogue stages the bf16 tile in the freed LDS with the token index
 // XOR-swizzled by the vocabulary-pair block, so that both output layouts leave
@@ -131,14 +139,33 @@ __device__ __forceinline__ void tile_coords(int group_m, int tiles_m, int tiles_
   tn = in_g / gm;
 }
 
-// The main loop: acc = A[m0:m0+256, 0:K] * B[n0:n0+256, 0:K]^T.
-// A rows >= M and B rows >= N are read from the last valid row (their results
-// are masked by the epilogues). Requires K % 64 == 0, lda and ldb multiples of
-// 8 elements, 16-byte aligned A and B, and 256*ld*2 < 2^32 bytes.
+// The main loop: acc = A[m0:m0+256, 0:K] * B[n0:n0+256, 0:K]^T, each operand
+// K-contiguous (A[m, k] at A + m * lda + k; kAMN = false) or MN-contiguous
+// (A[m, k] at A + k * lda + m; kAMN = true), and B likewise.
+// K-contiguous operands: rows >= M (N) are read from the last valid row; their
+// results are masked by the epilogues. MN-contiguous operands: columns are
+// read in 8-element chunks up to the one holding column M - 1 (N - 1), so the
+// rows must be allocated to a multiple of 8 elements past it; later chunks
+// repeat that one. An MN-contiguous operand may hold fewer k-rows than K
+// (ka_rows, kb_rows): k-rows past its last are read as its last, so the other
+// operand must hold zeros there. Requires K % 64 == 0, lda and ldb multiples of 8 elements,
+// 16-byte aligned A and B, and 256 * ld * 2 < 2^32 bytes (K-contiguous) or
+// 64 * ld * 2 < 2^32 bytes (MN-contiguous).
+//
+// LDS per stage and operand: 32 KiB. K-contiguous: 256 rows of 128 bytes (the
+// stage's 64 k), 16-byte chunks XOR-swizzled by (row >> 1) & 7, one
+// ds_read_b128 per fragment. MN-contiguous: 64 k-rows of 512 bytes (256
+// columns), chunk c of row k at c ^ 4 (k & 3); a fragment is two
+// ds_read_b64_tr_b16, each giving a lane 4 consecutive k of its column (in a
+// group of 16 lanes, lanes 4r .. 4r + 3 read 16 columns of k-row r and lane j
+// receives column j of the 4 rows), and the swizzle puts the 8 k-rows of one
+// read on distinct 16-byte bank groups, two rows per group.
+template <bool kAMN, bool kBMN>
 __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t lda,
                                               int64_t M, const uint16_t* __restrict__ B,
                                               int64_t ldb, int64_t N, int64_t K, int64_t m0,
-                                              int64_t n0, char* lds, Acc& acc) {
+                                              int64_t n0, char* lds, Acc& acc,
+                                              int64_t ka_rows = 0, int64_t kb_rows = 0) {
   const int lane = threadIdx.x & 63;
   // The wave index is uniform across the wave; say so, so that the load
   // bases and LDS destinations below live in scalar registers.
@@ -153,54 +180,99 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
       for (int e = 0; e < 16; ++e) acc.c[i][j][e] = 0.0f;
 
   // ---- load plan: this wave fills kBlocksPerWave 1 KiB blocks per stage ----
-  // Lane p of a block writes LDS bytes [16p, 16p+16): row p/8 of the block,
-  // physical chunk p%8, which holds logical chunk (p%8) ^ ((row >> 1) & 7).
+  // K-contiguous: lane p of a block writes LDS bytes [16p, 16p+16): row p/8 of
+  // the block, physical chunk p%8, which holds logical chunk
+  // (p%8) ^ ((row >> 1) & 7). MN-contiguous: a block is k-rows 2b and 2b + 1,
+  // lane p writes row 2b + p/32, physical chunk p%32, which holds logical
+  // chunk (p%32) ^ 4 (row & 3).
   const int first_block = wave * kBlocksPerWave;
   const bool load_a = first_block < kBlocksA;
-  const int row_lane = lane >> 3;
+  const bool mn_op = load_a ? kAMN : kBMN;
   const char* gbase;
-  int64_t ld_op, rows_op;
+  int64_t ld_op, rows_op, krows_op;
   int lds_op;
   int blk0;
   if (load_a) {
-    gbase = reinterpret_cast<const char*>(A + m0 * lda);
-    ld_op = lda; rows_op = M - m0; lds_op = 0; blk0 = first_block;
+    gbase = reinterpret_cast<const char*>(kAMN ? A + m0 : A + m0 * lda);
+    ld_op = lda; rows_op = M - m0; krows_op = ka_rows; lds_op = 0; blk0 = first_block;
   } else {
-    gbase = reinterpret_cast<const char*>(B + n0 * ldb);
-    ld_op = ldb; rows_op = N - n0; lds_op = kStageA; blk0 = first_block - kBlocksA;
+    gbase = reinterpret_cast<const char*>(kBMN ? B + n0 : B + n0 * ldb);
+    ld_op = ldb; rows_op = N - n0; krows_op = kb_rows; lds_op = kStageA;
+    blk0 = first_block - kBlocksA;
   }
   uint32_t goff[kBlocksPerWave];
+  // MN-contiguous: the lane's k-row within the stage and its (clamped)
+  // logical chunk, as a byte offset.
+  auto mn_row = [&](int j) { return 2 * (blk0 + j) + (lane >> 5); };
+  auto mn_chunk_bytes = [&](int j) {
+    const int last_chunk = static_cast<int>((rows_op + 7) / 8 - 1);  // >= 0
+    int chunk = (lane & 31) ^ (4 * (mn_row(j) & 3));
+    if (chunk > last_chunk) chunk = last_chunk;
+    return chunk * 16;
+  };
+  if ((kAMN || kBMN) && mn_op) {
 #pragma unroll
-  for (int j = 0; j < kBlocksPerWave; ++j) {
-    const int tile_row = (blk0 + j) * 8 + row_lane;
-    const int chunk = (lane & 7) ^ ((tile_row >> 1) & 7);
-    int64_t r = tile_row;
-    if (r > rows_op - 1) r = rows_op - 1;
-    goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
+    for (int j = 0; j < kBlocksPerWave; ++j)
+      goff[j] = static_cast<uint32_t>(mn_row(j) * ld_op * 2 + mn_chunk_bytes(j));
+  } else {
+    const int row_lane = lane >> 3;
+#pragma unroll
+    for (int j = 0; j < kBlocksPerWave; ++j) {
+      const int tile_row = (blk0 + j) * 8 + row_lane;
+      const int chunk = (lane & 7) ^ ((tile_row >> 1) & 7);
+      int64_t r = tile_row;
+      if (r > rows_op - 1) r = rows_op - 1;
+      goff[j] = static_cast<uint32_t>((r * ld_op + chunk * 8) * 2);
+    }
   }
 
   // Buffer resource on this wave's operand tile: base = the tile's first row,
   // no stride, no range limit (every offset above is clamped in bounds), gfx9
-  // data format word. The K position goes in the scalar offset, so a stage's
-  // loads need no per-lane address arithmetic.
-  const uint64_t gaddr = reinterpret_cast<uint64_t>(gbase);
+  // data format word. A K-contiguous operand's K position goes in the scalar
+  // offset, so a stage's loads need no per-lane address arithmetic; an
+  // MN-contiguous one moves the base by 64 rows per stage instead (the offset
+  // would pass 32 bits).
+  auto set_base = [](i32x4_t& r, const char* base) {
+    const uint64_t gaddr = reinterpret_cast<uint64_t>(base);
+    r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(gaddr & 0xffffffffu));
+    r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(gaddr >> 32));
+  };
   i32x4_t rsrc;
-  rsrc[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(gaddr & 0xffffffffu));
-  rsrc[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(gaddr >> 32));
+  set_base(rsrc, gbase);
   rsrc[2] = -1;
   rsrc[3] = 0x00020000;
   auto issue = [&](int stage, int64_t k0) {
     char* l = lds + stage * kStage + lds_op + blk0 * 1024;
-    const int soff = __builtin_amdgcn_readfirstlane(static_cast<int>(k0 * 2));
+    int soff = 0;
+    if ((kAMN || kBMN) && mn_op) {
+      if (k0 + kBK > krows_op) {
+        // The stage runs past the operand's k-rows: read from row
+        // min(k0, krows - 1) and clamp each lane's row to the last one.
+        const int64_t b0 = k0 < krows_op ? k0 : krows_op - 1;
+        set_base(rsrc, gbase + b0 * ld_op * 2);
+#pragma unroll
+        for (int j = 0; j < kBlocksPerWave; ++j) {
+          int64_t row = k0 + mn_row(j);
+          if (row > krows_op - 1) row = krows_op - 1;
+          const int off = static_cast<int>((row - b0) * ld_op * 2) + mn_chunk_bytes(j);
+          raw_buffer_load_lds(rsrc, (lds_void_t*)(l + j * 1024), 16, off, 0, 0, 0);
+        }
+        return;
+      }
+      set_base(rsrc, gbase + k0 * ld_op * 2);
+    } else {
+      soff = __builtin_amdgcn_readfirstlane(static_cast<int>(k0 * 2));
+    }
 #pragma unroll
     for (int j = 0; j < kBlocksPerWave; ++j)
       raw_buffer_load_lds(rsrc, (lds_void_t*)(l + j * 1024), 16, static_cast<int>(goff[j]), soff,
                           0, 0);
   };
 
-  // ---- fragment plan: 32x32x16 operands, 8 bf16 per lane -------------------
-  // A fragment fm, K sub-step s: row wm*128 + 32*fm + lane%32, logical chunk
-  // 2*s + lane/32 of that row (16 bytes).
+  // ---- fragment plan: 32x32x16 operands, 8 bf16 per lane (k 8 * (lane / 32)
+  // .. + 7 of the sub-step, row or column lane % 32 of the fragment) --------
+  // K-contiguous A fragment fm, K sub-step s: row wm*128 + 32*fm + lane%32,
+  // logical chunk 2*s + lane/32 of that row (16 bytes).
   const int frow = lane & 31;
   const int fhalf = lane >> 5;
   const int a_row_off = (wm * kWaveM + frow) * 128;
@@ -208,6 +280,30 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
   int xo[4];
 #pragma unroll
   for (int s = 0; s < 4; ++s) xo[s] = (((2 * s + fhalf) ^ ((frow >> 1) & 7)) << 4);
+  // MN-contiguous: lane 16 g + 4 r + u reads k-row 8 (g / 2) + r (+ 16 s + 4 h
+  // for sub-step s and half h), columns 16 (g % 2) + 4 u .. + 3 of the
+  // fragment: chunk (fragment base) / 8 + 2 (g % 2) + u / 2, 8 bytes in.
+  const int tg = lane >> 4, tr = (lane >> 2) & 3, tu = lane & 3;
+  const int tr_lane = (8 * (tg >> 1) + tr) * 512 + 8 * (tu & 1);
+  auto tr_off = [&](int col0) {  // col0: first column of the fragment, multiple of 32
+    return tr_lane + ((((col0 >> 3) + 2 * (tg & 1) + (tu >> 1)) ^ (4 * tr)) << 4);
+  };
+  int a_tr[kFM], b_tr[kFN];
+#pragma unroll
+  for (int i = 0; i < kFM; ++i) a_tr[i] = tr_off(wm * kWaveM + 32 * i);
+#pragma unroll
+  for (int j = 0; j < kFN; ++j) b_tr[j] = kStageA + tr_off(wn * kWaveN + 32 * j);
+
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef short s16x8_t __attribute__((ext_vector_type(8)));
+  auto read_tr = [](const char* p, int off) {
+    const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t*)(p + off));
+    const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s16x4_t*)(p + off + 4 * 512));
+    const s16x8_t v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(bf16x8_t, v);
+  };
 
   // Fragments of one K sub-step; two sets alternate so that the LDS reads of
   // sub-step s+1 are in flight under the 16 MFMAs of sub-step s.
@@ -217,11 +313,19 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
   };
   auto load_frags = [&](const char* st, int s, Frags& f) {
 #pragma unroll
-    for (int i = 0; i < kFM; ++i)
-      f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
+    for (int i = 0; i < kFM; ++i) {
+      if constexpr (kAMN)
+        f.a[i] = read_tr(st + 16 * s * 512, a_tr[i]);
+      else
+        f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
+    }
 #pragma unroll
-    for (int j = 0; j < kFN; ++j)
-      f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
+    for (int j = 0; j < kFN; ++j) {
+      if constexpr (kBMN)
+        f.b[j] = read_tr(st + 16 * s * 512, b_tr[j]);
+      else
+        f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
+    }
   };
   auto mma = [&](const Frags& f) {
 #pragma unroll
@@ -235,18 +339,35 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
       }
   };
 
-  // One sub-step of the pipeline: the LDS reads of the next fragments (8 of
-  // them) interleaved one per MFMA with the 16 MFMAs of the current ones, so
+  // One sub-step of the pipeline: the LDS reads of the next fragments
+  // interleaved with the 8 MFMAs of the current ones (one read per MFMA, two
+  // for the first MFMAs when an operand takes two reads per fragment), so
   // that the compiler neither serialises them nor reuses registers early.
+  constexpr int kReads = (kAMN ? 2 : 1) * kFM + (kBMN ? 2 : 1) * kFN;
+  constexpr int kMfmas = kFM * kFN;
+  static_assert(kReads <= 2 * kMfmas, "at most two reads per MFMA");
   auto step = [&](const char* st_next, int s_next, Frags& next, const Frags& cur) {
     load_frags(st_next, s_next, next);
     mma(cur);
+    if constexpr (kReads <= kMfmas) {
 #pragma unroll
-    for (int i = 0; i < kFM + kFN; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      for (int i = 0; i < kReads; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, kMfmas - kReads, 0);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kReads - kMfmas; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // 2 LDS reads
+      }
+#pragma unroll
+      for (int i = 0; i < 2 * kMfmas - kReads; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // 1 MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // 1 LDS read
+      }
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, kFM * kFN - (kFM + kFN), 0);
   };
 
   // Stage kt lives in LDS buffer kt & 1. Loads run one stage ahead: stage
@@ -282,7 +403,6 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
   }
   wait_vmem();
 }
-
 
 // Row (within the wave's 128 rows) of accumulator fm, element e, for this lane:
 // the 32x32 result gives lane l column l%32 and rows 8*(e/4) + 4*(l/32) + e%4.
@@ -355,7 +475,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_stats_kernel(
   tile_coords(kGroupMStats, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
-  gemm_mainloop(W, H, V, X, H, N, H, m0, n0, lds, acc);
+  gemm_mainloop<false, false>(W, H, V, X, H, N, H, m0, n0, lds, acc);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -474,7 +594,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   tile_coords(kGroupM, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
-  gemm_mainloop(Wc, H, Mvalid, X, H, N, H, m0, n0, lds, acc);
+  gemm_mainloop<false, false>(Wc, H, Mvalid, X, H, N, H, m0, n0, lds, acc);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -578,11 +698,11 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
 //   kMode 2: Cf += acc (fp32)
 //   kMode 3: C = bf16(Cf + acc)
 // ---------------------------------------------------------------------------
-template <int kMode>
+template <int kMode, bool kAMN = false, bool kBMN = false>
 __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
     const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
     int64_t ldb, int64_t N, int64_t K, uint16_t* __restrict__ C, float* __restrict__ Cf,
-    int64_t ldc, int group_m) {
+    int64_t ldc, int group_m, int64_t ka_rows, int64_t kb_rows) {
   extern __shared__ __align__(16) char lds[];
   const int tiles_m = static_cast<int>((M + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
@@ -590,7 +710,7 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
   tile_coords(group_m, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
-  gemm_mainloop(A, lda, M, B, ldb, N, K, m0, n0, lds, acc);
+  gemm_mainloop<kAMN, kBMN>(A, lda, M, B, ldb, N, K, m0, n0, lds, acc, ka_rows, kb_rows);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -690,7 +810,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
   tile_coords(kGroupMStats, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
-  gemm_mainloop(W, H, V, X, H, N, H, m0, n0, lds, acc);
+  gemm_mainloop<false, false>(W, H, V, X, H, N, H, m0, n0, lds, acc);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -830,30 +950,21 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
 // statistics (M, T1) are combined (cross_entropy.py:53-65):
 //   dZ[t, v] = exp(z - M) / (1 + T1) * g = pt[v, t] * exp(pmax[b, t] - M) * g / (1 + T1)
 // and, on the target row, (softmax - 1) * g from the fp32 target logit
-// (target_grad). Written in place into pt (vocabulary-major, the dW GEMM's A)
-// and transposed into dz [N, ldz] (token-major, the dX GEMM's A). A workgroup
-// takes one 128-row block of partial statistics and 256 tokens; the factor of
-// each (block, token) is formed once. Rows past V and blocks past nb come out
-// 0 (pt holds 0 there), tokens past N are not written to dz.
+// (target_grad), written in place into pt, which both backward products then
+// read as it lies (vocabulary-major). A workgroup takes one 128-row block of
+// partial statistics and 256 tokens; the factor of each (block, token) is
+// formed once. Rows past V and blocks past nb come out 0 (pt holds 0 there).
 // ---------------------------------------------------------------------------
 constexpr int kRsRows = kPartialRows;  // 128: one block of partial statistics
 constexpr int kRsToks = 256;
-constexpr int kRsLdsBytes = kRsToks * (kRsRows / 2) * 4;  // the tile, 64 KiB
 __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
-    uint16_t* __restrict__ pt, int64_t ldt, uint16_t* __restrict__ dz, int64_t ldz, int64_t V,
-    int64_t N, const float* __restrict__ pmax, int64_t nb, const float* __restrict__ gmax,
-    const float* __restrict__ gsum1, const float* __restrict__ tlogit,
-    const int64_t* __restrict__ target, int64_t vstart, const float* __restrict__ gout,
-    int64_t gstride, float gdiv) {
+    uint16_t* __restrict__ pt, int64_t ldt, int64_t V, int64_t N, const float* __restrict__ pmax,
+    int64_t nb, const float* __restrict__ gmax, const float* __restrict__ gsum1,
+    const float* __restrict__ tlogit, const int64_t* __restrict__ target, int64_t vstart,
+    const float* __restrict__ gout, int64_t gstride, float gdiv) {
   __shared__ float s_scale[kRsToks];
   __shared__ float s_dt[kRsToks];
   __shared__ int s_tv[kRsToks];
-  // The tile (dynamic LDS, kRsLdsBytes), token-major, as words of two
-  // vocabulary rows: word q of token t holds rows 2q (low half) and 2q + 1
-  // (high half), at t * 64 + (q ^ 4 ((t >> 3) & 15)). The XOR spreads the
-  // 16-byte reads of the dz pass over all 64 banks, and the word writes of
-  // the pt pass over 32 of them (two-way conflicts).
-  extern __shared__ __align__(16) uint32_t tile[];
   const int64_t blk = blockIdx.x;
   const int64_t v0 = blk * kRsRows;
   const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kRsToks;
@@ -879,10 +990,9 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
   __syncthreads();
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  // pt pass: a lane takes tokens 8s .. 8s + 7 of two adjacent rows per
-  // iteration; a wave's load covers two rows' 512-byte segments (256-byte
-  // ones ran 1% slower over the step). The last tile of a row may stop at ldt
-  // (a multiple of 64) partway.
+  // A lane takes tokens 8s .. 8s + 7 of two adjacent rows per iteration; a
+  // wave's load covers two rows' 512-byte segments. The last tile of a row
+  // may stop at ldt (a multiple of 64) partway.
   const int sg = lane & 31;
   const int tg = 8 * sg;
   const bool tok_ok = t0 + tg < ldt;
@@ -897,50 +1007,21 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
       f[k] = (s_tv[tg + k] == r) ? s_dt[tg + k] : f[k];
     }
   };
-#pragma unroll
+  if (!tok_ok) return;
+#pragma unroll 4
   for (int it = 0; it < kRsRows / 2 / 8; ++it) {
-    const int q = (lane >> 5) + 2 * (wave + 4 * it);  // row pair
-    const int r = 2 * q;
+    const int r = 2 * ((lane >> 5) + 2 * (wave + 4 * it));  // even row of the pair
     u32x4* p0 = reinterpret_cast<u32x4*>(pt + (v0 + r) * ldt + t0 + tg);
     u32x4* p1 = reinterpret_cast<u32x4*>(pt + (v0 + r + 1) * ldt + t0 + tg);
-    u32x4 a = {0u, 0u, 0u, 0u}, b = {0u, 0u, 0u, 0u};
-    if (tok_ok) {
-      a = *p0;
-      b = *p1;
-    }
+    const u32x4 a = *p0;
+    const u32x4 b = *p1;
     float fa[8], fb[8];
     Elem<uint16_t>::unpack(a, fa);
     Elem<uint16_t>::unpack(b, fb);
     fix(fa, r);
     fix(fb, r + 1);
-    const u32x4 wa = Elem<uint16_t>::pack(fa);
-    const u32x4 wb = Elem<uint16_t>::pack(fb);
-    if (tok_ok) {
-      *p0 = wa;
-      *p1 = wb;
-    }
-    const uint32_t la[4] = {wa.x, wa.y, wa.z, wa.w};
-    const uint32_t lb[4] = {wb.x, wb.y, wb.z, wb.w};
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t lo = (k & 1) ? (la[k >> 1] >> 16) : (la[k >> 1] & 0xffffu);
-      const uint32_t hi = (k & 1) ? (lb[k >> 1] & 0xffff0000u) : (lb[k >> 1] << 16);
-      const int t = tg + k;
-      tile[t * 64 + (q ^ (4 * ((t >> 3) & 15)))] = lo | hi;
-    }
-  }
-  __syncthreads();
-  // dz pass: token rows of 128 vocabulary entries (16 chunks of 16 bytes); a
-  // wave's store covers four tokens' 256-byte segments.
-#pragma unroll
-  for (int it = 0; it < kRsToks / 16; ++it) {
-    const int t = (lane >> 4) + 4 * (wave + 4 * it);
-    const int w = lane & 15;
-    if (t0 + t < N) {
-      const int sw = (t >> 3) & 15;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(&tile[t * 64 + 4 * (w ^ sw)]);
-      *reinterpret_cast<u32x4*>(dz + (t0 + t) * ldz + v0 + 8 * w) = v;
-    }
+    *p0 = Elem<uint16_t>::pack(fa);
+    *p1 = Elem<uint16_t>::pack(fb);
   }
 }
 
@@ -1019,16 +1100,17 @@ int configure_lds() {
       reinterpret_cast<const void*>(&gemm_store_kernel<1>),
       reinterpret_cast<const void*>(&gemm_store_kernel<2>),
       reinterpret_cast<const void*>(&gemm_store_kernel<3>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<0, true, true>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<0, false, true>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<1, false, true>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<2, false, true>),
+      reinterpret_cast<const void*>(&gemm_store_kernel<3, false, true>),
   };
   for (const void* k : kernels) {
     const hipError_t e =
         hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return static_cast<int>(e);
   }
-  const hipError_t e =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&lmhead_dz_rescale_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, kRsLdsBytes);
-  if (e != hipSuccess) return static_cast<int>(e);
   lds_configured = true;
   return NMCE_OK;
 }
@@ -1039,17 +1121,45 @@ inline bool operand_ok(const void* p, int64_t ld) {
   return p != nullptr && aligned16(p) && ld % 8 == 0 && ld > 0 && ld < (int64_t{1} << 22);
 }
 
+// The product kernels by output mode and operand layout: K-contiguous A, and
+// B K-contiguous (b_mn = false) or MN-contiguous with kb_rows k-rows (b_mn;
+// then A may be MN-contiguous too, a_mn, in mode 0 only).
+template <int kMode, bool kAMN, bool kBMN>
+void launch_store(dim3 grid, hipStream_t stream, const uint16_t* A, int64_t lda, int64_t M,
+                  const uint16_t* B, int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf,
+                  int64_t ldc, int group_m, int64_t ka_rows, int64_t kb_rows) {
+  hipLaunchKernelGGL((gemm_store_kernel<kMode, kAMN, kBMN>), grid, dim3(kThreads), kLdsBytes,
+                     stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m, ka_rows, kb_rows);
+}
+
 int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const uint16_t* B,
                       int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf, int64_t ldc,
-                      hipStream_t stream, int group_m = kGroupM) {
+                      hipStream_t stream, int group_m = kGroupM, bool a_mn = false,
+                      bool b_mn = false, int64_t ka_rows = 0, int64_t kb_rows = 0) {
   const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
   const dim3 grid(static_cast<unsigned>(tiles));
-  switch (mode) {
-    case 0: hipLaunchKernelGGL(gemm_store_kernel<0>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
-    case 1: hipLaunchKernelGGL(gemm_store_kernel<1>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
-    case 2: hipLaunchKernelGGL(gemm_store_kernel<2>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
-    default: hipLaunchKernelGGL(gemm_store_kernel<3>, grid, dim3(kThreads), kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m); break;
+  if (a_mn && (!b_mn || mode != 0)) return NMCE_EINVAL_SHAPE;
+#define NMCE_STORE(MODE, AMN, BMN)                                                        \
+  launch_store<MODE, AMN, BMN>(grid, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m, \
+                               ka_rows, kb_rows)
+  if (a_mn) {
+    NMCE_STORE(0, true, true);
+  } else if (b_mn) {
+    switch (mode) {
+      case 0: NMCE_STORE(0, false, true); break;
+      case 1: NMCE_STORE(1, false, true); break;
+      case 2: NMCE_STORE(2, false, true); break;
+      default: NMCE_STORE(3, false, true); break;
+    }
+  } else {
+    switch (mode) {
+      case 0: NMCE_STORE(0, false, false); break;
+      case 1: NMCE_STORE(1, false, false); break;
+      case 2: NMCE_STORE(2, false, false); break;
+      default: NMCE_STORE(3, false, false); break;
+    }
   }
+#undef NMCE_STORE
   return launch_status();
 }
 
@@ -1096,10 +1206,10 @@ int64_t fwd_partial_blocks(int64_t v) { return (v + kPartialRows - 1) / kPartial
 struct FusedLayout {
   int64_t chunk;     // tokens per chunk (the last one may hold fewer)
   int64_t n_chunks;
-  int64_t ldt;       // chunk tokens padded to 64: row stride of P^T and X^T, K of the dW GEMM
+  int64_t ldt;       // chunk tokens padded to 64: row stride of P^T, K of the dW GEMM
   int64_t vpad;      // vocabulary padded to 256: rows of P^T, K of the dX GEMM
   int64_t nb;        // 128-row blocks of partial statistics
-  int64_t off_wt, off_xt, off_pt, off_dz, off_part, off_acc, total;
+  int64_t off_pt, off_part, off_acc, total;
 };
 
 FusedLayout fused_layout(int64_t n, int64_t h, int64_t v, int64_t token_chunk) {
@@ -1111,10 +1221,7 @@ FusedLayout fused_layout(int64_t n, int64_t h, int64_t v, int64_t token_chunk) {
   L.vpad = round_up(v, kBM);
   L.nb = fwd_partial_blocks(v);
   int64_t off = 0;
-  L.off_wt = off; off += align256(h * L.vpad * 2);
-  L.off_xt = off; off += align256(h * L.ldt * 2);
   L.off_pt = off; off += align256(L.vpad * L.ldt * 2);
-  L.off_dz = off; off += align256(L.chunk * L.vpad * 2);
   L.off_part = off; off += align256(3 * L.nb * L.chunk * 4);
   L.off_acc = off; off += L.n_chunks > 1 ? align256(v * h * 4) : 0;
   L.total = off;
@@ -1437,8 +1544,7 @@ int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t voc
   if (n_rows < 1 || hidden_size < 1 || vocab_local < 1) return NMCE_EINVAL_SHAPE;
   const FusedLayout L = fused_layout(n_rows, hidden_size, vocab_local, token_chunk);
   const int64_t v[NMCE_LMHEAD_FUSED_LAYOUT_FIELDS] = {
-      L.total, L.chunk, L.n_chunks, L.ldt, L.vpad, L.nb, L.off_wt, L.off_xt, L.off_pt, L.off_dz,
-      L.off_part, L.off_acc};
+      L.total, L.chunk, L.n_chunks, L.ldt, L.vpad, L.nb, L.off_pt, L.off_part, L.off_acc};
   for (int i = 0; i < NMCE_LMHEAD_FUSED_LAYOUT_FIELDS; ++i) layout[i] = v[i];
   return NMCE_OK;
 }
@@ -1448,21 +1554,6 @@ int nmce_hint_assume(const float* hint, float* assumed, void* stream) {
   hipLaunchKernelGGL(hint_assume_kernel, dim3(1), dim3(64), 0, static_cast<hipStream_t>(stream),
                      hint, assumed);
   return launch_status();
-}
-
-int nmce_lmhead_ce_fused_prepare(const void* hidden, const void* weight, int dtype,
-                                 int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
-                                 int64_t token_chunk, void* workspace, int64_t workspace_bytes,
-                                 void* stream) {
-  FusedLayout L;
-  int st = check_fused_args(hidden, weight, dtype, n_rows, hidden_size, vocab_local, token_chunk,
-                            workspace, workspace_bytes, L);
-  if (st) return st;
-  char* ws = static_cast<char*>(workspace);
-  // W^T [H, vpad], zero beyond the shard's rows: the dX GEMM's B operand.
-  return launch_transpose(static_cast<const uint16_t*>(weight), vocab_local, hidden_size,
-                          hidden_size, reinterpret_cast<uint16_t*>(ws + L.off_wt), L.vpad,
-                          static_cast<hipStream_t>(stream));
 }
 
 int nmce_lmhead_ce_fused_chunk_stats(const void* hidden, const void* weight, int dtype,
@@ -1524,37 +1615,37 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
   const int64_t nc = (n_rows - t0) < L.chunk ? (n_rows - t0) : L.chunk;
   const int64_t H = hidden_size, V = vocab_local;
   const auto* X = static_cast<const uint16_t*>(hidden);
+  const auto* W = static_cast<const uint16_t*>(weight);
   auto* pt = reinterpret_cast<uint16_t*>(ws + L.off_pt);
-  auto* dz = reinterpret_cast<uint16_t*>(ws + L.off_dz);
-  auto* xt = reinterpret_cast<uint16_t*>(ws + L.off_xt);
-  const auto* wt = reinterpret_cast<const uint16_t*>(ws + L.off_wt);
   const float* pmax = reinterpret_cast<const float*>(ws + L.off_part);
-  // dZ of the chunk, vocabulary-major in place of P^T and token-major into dz.
+  // dZ^T of the chunk, in place of P^T.
   hipLaunchKernelGGL(lmhead_dz_rescale_kernel,
                      dim3(static_cast<unsigned>(L.vpad / kRsRows),
                           static_cast<unsigned>((L.ldt + kRsToks - 1) / kRsToks)),
-                     dim3(256), kRsLdsBytes, s, pt, L.ldt, dz, L.vpad, V, nc, pmax, L.nb, g_max + t0,
-                     g_sumexp_m1 + t0, target_logit + t0, target + t0, vocab_start,
-                     grad_output + t0 * gout_stride, gout_stride, gout_div);
+                     dim3(256), 0, s, pt, L.ldt, V, nc, pmax, L.nb, g_max + t0, g_sumexp_m1 + t0,
+                     target_logit + t0, target + t0, vocab_start, grad_output + t0 * gout_stride,
+                     gout_stride, gout_div);
   if ((st = launch_status())) return st;
-  // X_c^T [H, ldt], zero beyond the chunk's tokens: the dW GEMM's B operand.
-  if ((st = launch_transpose(X + t0 * H, nc, H, H, xt, L.ldt, s))) return st;
-  // dX rows of the chunk = dZ_c W (K = the padded vocabulary; the padding of
-  // dz and W^T is zero).
-  if ((st = launch_gemm_store(0, dz, L.vpad, nc, wt, L.vpad, H, L.vpad,
+  // dX rows of the chunk = dZ_c W: both operands read as they lie, k-row
+  // (vocabulary) major: dZ^T [vpad, ldt] and W [V, H] (K = the padded
+  // vocabulary; dZ^T is zero past V, so W's k-rows stop at V).
+  if ((st = launch_gemm_store(0, pt, L.ldt, nc, W, H, H, L.vpad,
                               static_cast<uint16_t*>(grad_hidden) + t0 * H, nullptr, H, s,
-                              kGroupMProducts)))
+                              kGroupMProducts, true, true, L.vpad, V)))
     return st;
-  // dW (+)= dZ_c^T X_c (K = the chunk's padded tokens), accumulated in fp32
-  // across chunks and rounded to bf16 by the last.
+  // dW (+)= dZ_c^T X_c: A = dZ^T (K = the chunk's padded tokens contiguous),
+  // B = the chunk's rows of X as they lie, token-major (zero dZ^T columns past
+  // the chunk, so X's k-rows stop at nc). Accumulated in fp32 across chunks
+  // and rounded to bf16 by the last.
   int mode;
   if (L.n_chunks == 1) mode = 0;
   else if (chunk_index == 0) mode = 1;
   else if (chunk_index + 1 < L.n_chunks) mode = 2;
   else mode = 3;
-  return launch_gemm_store(mode, pt, L.ldt, V, xt, L.ldt, H, L.ldt,
+  return launch_gemm_store(mode, pt, L.ldt, V, X + t0 * H, H, H, L.ldt,
                            static_cast<uint16_t*>(grad_weight),
-                           reinterpret_cast<float*>(ws + L.off_acc), H, s, kGroupMProducts);
+                           reinterpret_cast<float*>(ws + L.off_acc), H, s, kGroupMProducts, false,
+                           true, 0, nc);
 }
 
 }  // extern "C"
@@ -1575,4 +1666,23 @@ extern "C" int nmce_gemm_nt_bf16(const void* a, int64_t lda, const void* b, int6
                            static_cast<const uint16_t*>(b), ldb, n, k,
                            static_cast<uint16_t*>(c), static_cast<float*>(c), ldc,
                            static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nmce_gemm_mn_bf16(int a_mn, const void* a, int64_t lda, const void* b,
+                                 int64_t ldb, int64_t m, int64_t n, int64_t k, void* c,
+                                 int64_t ldc, void* stream) {
+  if (m < 0 || n < 0 || k <= 0 || k % kBK != 0) return NMCE_EINVAL_SHAPE;
+  if (m == 0 || n == 0) return NMCE_OK;
+  const bool a_ok = a_mn ? lda >= (m + 7) / 8 * 8 && 64 * lda < (int64_t{1} << 31) : lda >= k;
+  if (!operand_ok(a, lda) || !operand_ok(b, ldb) || !a_ok || ldb < (n + 7) / 8 * 8 ||
+      64 * ldb >= (int64_t{1} << 31))
+    return NMCE_EINVAL_ALIGN;
+  if (!c || ldc < n) return NMCE_EINVAL_PTR;
+  if (m > (int64_t{1} << 30) || n > (int64_t{1} << 30)) return NMCE_EINVAL_SHAPE;
+  int st = configure_lds();
+  if (st) return st;
+  return launch_gemm_store(0, static_cast<const uint16_t*>(a), lda, m,
+                           static_cast<const uint16_t*>(b), ldb, n, k, static_cast<uint16_t*>(c),
+                           nullptr, ldc, static_cast<hipStream_t>(stream), kGroupM, a_mn != 0,
+                           true, k, k);
 }

@@ -55,14 +55,13 @@ SIGNATURES: dict[str, tuple] = {
                                     _p, _p, _i64, _p, _i64, _p]),
     "nmce_lmhead_ce_fused_layout": (_c_int, [_i64, _i64, _i64, _i64, _p]),
     "nmce_hint_assume": (_c_int, [_p, _p, _p]),
-    "nmce_lmhead_ce_fused_prepare": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64,
-                                              _p]),
     "nmce_lmhead_ce_fused_chunk_stats": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64,
                                                   _i64, _i64, _p, _p, _p, _p, _i64, _p]),
     "nmce_lmhead_ce_fused_chunk_grads": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64,
                                                   _i64, _i64, _p, _p, _p, _p, _i64,
                                                   ctypes.c_float, _p, _p, _p, _i64, _p]),
     "nmce_gemm_nt_bf16": (_c_int, [_p, _i64, _p, _i64, _i64, _i64, _i64, _p, _c_int, _i64, _p]),
+    "nmce_gemm_mn_bf16": (_c_int, [_c_int, _p, _i64, _p, _i64, _i64, _i64, _i64, _p, _i64, _p]),
     "nmce_lmhead_ce_bwd_layout": (_c_int, [_i64, _i64, _i64, _i64, _p]),
     "nmce_lmhead_ce_bwd_prepare": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p]),
     "nmce_lmhead_ce_bwd_dz": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p,
@@ -70,7 +69,7 @@ SIGNATURES: dict[str, tuple] = {
 }
 
 NMCE_LMHEAD_LAYOUT_FIELDS = 10
-NMCE_LMHEAD_FUSED_LAYOUT_FIELDS = 12
+NMCE_LMHEAD_FUSED_LAYOUT_FIELDS = 9
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

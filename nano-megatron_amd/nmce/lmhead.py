@@ -72,19 +72,19 @@ DEFAULT_VOCAB_CHUNK = 32768
 BACKWARD_GEMM = "nmce"
 
 # Bytes the one-pass path may hold for one chunk of tokens: the chunk's
-# exponentials and its dZ, 4 * chunk * V bytes (bf16). The default chunk is
-# the most tokens (a multiple of 256) within this budget, all of them when they
-# fit: a 16384-token micro-batch at V = 256000 takes 15.6 GiB of a 288 GB
-# device, less than the reference's fp32 logits and softmax for the same
-# tokens. One chunk needs no fp32 accumulation of dW across chunks, which cost
-# 3% of the step at [16384, 4096] x [128256, 4096] and 10% at
+# exponentials, turned into its dZ^T in place, 2 * chunk * V bytes (bf16). The
+# default chunk is the most tokens (a multiple of 256) within this budget, all
+# of them when they fit: a 16384-token micro-batch at V = 256000 takes 7.8 GiB
+# of a 288 GB device, a quarter of the reference's fp32 logits and softmax for
+# the same tokens. One chunk needs no fp32 accumulation of dW across chunks,
+# which cost 3% of the step at [16384, 4096] x [128256, 4096] and 10% at
 # [16384, 3072] x [256000, 3072] (two chunks of 8192 against one of 16384).
 CHUNK_BUDGET_BYTES = 16 << 30
 
 
 def default_token_chunk(n_tokens: int, vocab_local: int) -> int:
     """Tokens per one-pass chunk within ``CHUNK_BUDGET_BYTES``."""
-    fit = CHUNK_BUDGET_BYTES // (4 * max(1, vocab_local)) // 256 * 256
+    fit = CHUNK_BUDGET_BYTES // (2 * max(1, vocab_local)) // 256 * 256
     return n_tokens if fit >= n_tokens else max(256, fit)
 
 _ALIGN = 64  # hidden size granularity of the GEMM kernels
@@ -177,8 +177,7 @@ def _fused_layout(lib, n: int, hp: int, v: int, token_chunk: int) -> dict:
     buf = (ctypes.c_int64 * _lib.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
     _lib.check(lib.nmce_lmhead_ce_fused_layout(n, hp, v, token_chunk, ctypes.addressof(buf)),
                "nmce_lmhead_ce_fused_layout")
-    keys = ("total", "chunk", "n_chunks", "ldt", "vpad", "nb", "off_wt", "off_xt", "off_pt",
-            "off_dz", "off_part", "off_acc")
+    keys = ("total", "chunk", "n_chunks", "ldt", "vpad", "nb", "off_pt", "off_part", "off_acc")
     return dict(zip(keys, (int(b) for b in buf)))
 
 
@@ -246,8 +245,6 @@ class _LMHeadVocabParallelCrossEntropyMean(torch.autograd.Function):
         assumed = torch.empty(1, dtype=torch.float32, device=dev)
         _launch("nmce_hint_assume", lib.nmce_hint_assume, hint.data_ptr(), assumed.data_ptr(),
                 stream)
-        _launch("nmce_lmhead_ce_fused_prepare", lib.nmce_lmhead_ce_fused_prepare, *args, chunk,
-                ws.data_ptr(), ws.numel(), stream)
         local = torch.empty((3, n), dtype=torch.float32, device=dev)  # max, sum - 1, target z
         out = torch.empty((3, n), dtype=torch.float32, device=dev)    # loss, max, sum - 1
         dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)

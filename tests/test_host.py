@@ -91,6 +91,12 @@ def test_lmhead_argument_errors_before_launch(lib):
     assert lib.nmce_gemm_nt_bf16(p, 64, p, 64, 16, 16, 100, p, 0, 16, None) == -2
     assert lib.nmce_gemm_nt_bf16(p, 64, p, 64, 16, 16, 64, p, 7, 16, None) == -1
     assert lib.nmce_gemm_nt_bf16(p, 60, p, 64, 16, 16, 64, p, 0, 16, None) == -3
+    mn = lib.nmce_gemm_mn_bf16
+    assert mn(1, p, 16, p, 16, 16, 16, 100, p, 16, None) == -2  # k not a multiple of 64
+    assert mn(1, p, 8, p, 16, 16, 16, 64, p, 16, None) == -3    # lda below m rounded to 8
+    assert mn(0, p, 32, p, 16, 16, 16, 64, p, 16, None) == -3   # K-contiguous a: lda < k
+    assert mn(1, p, 16, p, 8, 16, 16, 64, p, 16, None) == -3    # ldb below n rounded to 8
+    assert mn(1, p, 16, p, 16, 16, 16, 64, None, 16, None) == -4
 
 
 def test_lmhead_workspace_layout(lib):
@@ -133,7 +139,7 @@ def test_default_chunk_never_holds_full_logits(lib):
 
 def test_one_pass_token_chunk_budget(lib):
     """The one-pass path's default token chunk: every token while the chunk's
-    exponentials and dZ (4 V bytes per token) fit the budget, else the most
+    exponentials, dZ^T once rescaled (2 V bytes per token), fit the budget, else the most
     multiples of 256 that do; the fused layout then holds one chunk (no fp32
     dW accumulator) or several (with one)."""
     import ctypes
@@ -145,17 +151,19 @@ def test_one_pass_token_chunk_budget(lib):
     for n, v in ((65536, 256000), (1 << 20, 128256), (40000, 1000000)):
         c = chunk(n, v)
         assert c < n and c % 256 == 0
-        assert 4 * v * c <= budget < 4 * v * (c + 256)
+        assert 2 * v * c <= budget < 2 * v * (c + 256)
     assert chunk(100, 1 << 40) == 256  # at least one tile column
     buf = (ctypes.c_int64 * L.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
-    # fields: total, chunk, n_chunks, ldt, vpad, nb, off_wt, off_xt, off_pt, off_dz, off_part, off_acc
+    # fields: total, chunk, n_chunks, ldt, vpad, nb, off_pt, off_part, off_acc
     assert lib.nmce_lmhead_ce_fused_layout(16384, 4096, 128256, chunk(16384, 128256),
                                            ctypes.addressof(buf)) == 0
-    assert (buf[1], buf[2]) == (16384, 1) and buf[11] == buf[0]  # no accumulator region
+    assert (buf[1], buf[2]) == (16384, 1) and buf[8] == buf[0]  # no accumulator region
+    # P^T [vpad, ldt] bf16 is the only chunk-sized buffer: no transposed copies
+    assert buf[7] - buf[6] == 128256 * 16384 * 2
     n, v = 65536, 256000
     assert lib.nmce_lmhead_ce_fused_layout(n, 3072, v, chunk(n, v), ctypes.addressof(buf)) == 0
-    assert buf[2] > 1 and buf[0] - buf[11] >= v * 3072 * 4  # fp32 dW accumulator
-    regions = [buf[6], buf[7], buf[8], buf[9], buf[10], buf[11]]
+    assert buf[2] > 1 and buf[0] - buf[8] >= v * 3072 * 4  # fp32 dW accumulator
+    regions = [buf[6], buf[7], buf[8]]
     assert all(r % 256 == 0 for r in regions) and regions == sorted(regions)
 
 

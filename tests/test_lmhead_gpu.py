@@ -198,6 +198,43 @@ def test_gemm_nt(m, n, k, out):
     assert (err <= bound).all(), f"max err {err.max():.3e} (bound {np.min(bound):.3e})"
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 256, 64), (300, 520, 128), (1000, 777, 320),
+                                   (1, 3, 64), (999, 1001, 1024)])
+@pytest.mark.parametrize("a_mn", [1, 0])
+def test_gemm_mn_is_the_nt_product_of_the_transposes(m, n, k, a_mn):
+    """The MN-contiguous operand path (ds_read_b64_tr_b16 fragments, used by
+    the fused backward products on dZ^T, W and X as they lie) gives the same
+    bits as the K-contiguous one on the transposed operands: every lane's
+    fragment holds the same 8 values in the same k order. Columns past m and
+    n (up to the 8-element padding) hold NaN, which the product must not
+    read into any written output."""
+    from nmce import _lib as L
+    lib = L.load()
+    print(f"[gemm mn] m={m} n={n} k={k} a_mn={a_mn}", flush=True)
+    g = _gen(m * 5 + n * 11 + k + a_mn)
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
+    b = torch.randn(n, k, generator=g).to(torch.bfloat16).to(DEV)
+    lda = (m + 7) // 8 * 8 + 8 if a_mn else k
+    ldb = (n + 7) // 8 * 8
+    if a_mn:
+        a_s = torch.full((k, lda), float("nan"), dtype=torch.bfloat16, device=DEV)
+        a_s[:, :m] = a.t()
+    else:
+        a_s = a
+    b_s = torch.full((k, ldb), float("nan"), dtype=torch.bfloat16, device=DEV)
+    b_s[:, :n] = b.t()
+    stream = L.stream_handle(torch.device(DEV))
+    c_mn = torch.full((m, n + 5), float("nan"), dtype=torch.bfloat16, device=DEV)
+    c_nt = torch.full((m, n), float("nan"), dtype=torch.bfloat16, device=DEV)
+    L.check(lib.nmce_gemm_mn_bf16(a_mn, a_s.data_ptr(), lda, b_s.data_ptr(), ldb, m, n, k,
+                                  c_mn.data_ptr(), n + 5, stream), "gemm mn")
+    L.check(lib.nmce_gemm_nt_bf16(a.data_ptr(), k, b.data_ptr(), k, m, n, k, c_nt.data_ptr(),
+                                  L.NMCE_BF16, n, stream), "gemm nt")
+    torch.cuda.synchronize()
+    assert torch.equal(c_mn[:, :n].view(torch.int16), c_nt.view(torch.int16))
+    assert torch.isnan(c_mn[:, n:].float()).all(), "wrote past n"
+
+
 def test_gemm_rejects_bad_k():
     from nmce import _lib as L
     lib = L.load()
