@@ -1013,15 +1013,16 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
     const int r = 2 * ((lane >> 5) + 2 * (wave + 4 * it));  // even row of the pair
     u32x4* p0 = reinterpret_cast<u32x4*>(pt + (v0 + r) * ldt + t0 + tg);
     u32x4* p1 = reinterpret_cast<u32x4*>(pt + (v0 + r + 1) * ldt + t0 + tg);
-    const u32x4 a = *p0;
-    const u32x4 b = *p1;
+    // Non-temporal both ways: P^T is gigabytes, read and written once here.
+    const u32x4 a = load_stream(p0);
+    const u32x4 b = load_stream(p1);
     float fa[8], fb[8];
     Elem<uint16_t>::unpack(a, fa);
     Elem<uint16_t>::unpack(b, fb);
     fix(fa, r);
     fix(fb, r + 1);
-    *p0 = Elem<uint16_t>::pack(fa);
-    *p1 = Elem<uint16_t>::pack(fb);
+    store_stream(p0, Elem<uint16_t>::pack(fa));
+    store_stream(p1, Elem<uint16_t>::pack(fb));
   }
 }
 
