@@ -1527,8 +1527,10 @@ int check_fused_args(const void* hidden, const void* weight, int dtype, int64_t 
   if (!operand_ok(hidden, hidden_size) || !operand_ok(weight, hidden_size))
     return NMCE_EINVAL_ALIGN;
   L = fused_layout(n_rows, hidden_size, vocab_local, token_chunk);
-  // 256 rows of every GEMM operand must span less than 4 GiB (32-bit offsets).
-  if (!operand_ok(weight, L.vpad) || L.ldt >= (int64_t{1} << 22)) return NMCE_EINVAL_SHAPE;
+  // Per-lane offsets are 32-bit: 256 rows of P^T (dW's K-contiguous A) and 64
+  // k-rows of P^T, W and X (MN-contiguous operands) must stay below 2 GiB;
+  // ldt < 2^22 covers P^T, and operand_ok above bounds H.
+  if (L.ldt >= (int64_t{1} << 22)) return NMCE_EINVAL_SHAPE;
   if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
     return NMCE_EINVAL_WORKSPACE;
   return NMCE_OK;
