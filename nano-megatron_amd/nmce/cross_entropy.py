@@ -55,6 +55,7 @@ must be built; anything else raises.
 from __future__ import annotations
 
 import sys
+import threading
 
 import torch
 import torch.distributed as dist
@@ -146,33 +147,59 @@ def _check_inputs(logits: torch.Tensor, target: torch.Tensor, vocab_start: int,
 _CHECK_POLLS = 200
 
 
+# Pinned count buffers and their events, per device, reused once a check is
+# over (allocating them cost a few microseconds per call, which a small batch
+# pays every step).
+_check_free: dict[int, list] = {}
+_check_lock = threading.Lock()
+
+
+def _check_slot(dev_index: int, slots: int):
+    with _check_lock:
+        free = _check_free.setdefault(dev_index, [])
+        for i, (host, event) in enumerate(free):
+            if host.numel() >= slots:
+                return free.pop(i)
+    cap = 1 << max(slots - 1, 0).bit_length()
+    return torch.empty(cap, dtype=torch.int32, pin_memory=True), torch.cuda.Event()
+
+
 class _PendingCheck:
     """Bad-target counts on their way to pinned host memory.
 
     The check kernel writes the counts straight into ``host`` (pinned memory
     is mapped into the device's address space at its host address), so the
-    buffer must stay alive until ``event`` has completed: every caller ends
+    buffer must not be reused until ``event`` has completed: every caller ends
     with ``raise_if_bad()`` or, when it leaves early on an exception,
-    ``wait()``.
+    ``wait()``, which return the buffer and the event to the per-device pool.
     """
 
-    def __init__(self, host: torch.Tensor, event: torch.cuda.Event):
+    def __init__(self, dev_index: int, host: torch.Tensor, event: torch.cuda.Event, slots: int):
+        self.dev_index = dev_index
         self.host = host
         self.event = event
+        self.slots = slots
+        self.bad = None
 
     def wait(self) -> None:
+        if self.bad is not None:
+            return
         # The counts usually reach the host within microseconds of the call:
         # poll first, so that a blocking wait's wake-up latency (tens of
         # microseconds, per step of a small batch) is paid only by long waits.
         event = self.event
         for _ in range(_CHECK_POLLS):
             if event.query():
-                return
-        event.synchronize()
+                break
+        else:
+            event.synchronize()
+        self.bad = bool(self.host.numpy()[:self.slots].any())
+        with _check_lock:
+            _check_free.setdefault(self.dev_index, []).append((self.host, self.event))
 
     def raise_if_bad(self) -> None:
         self.wait()
-        if int(self.host.sum()) != 0:
+        if self.bad:
             raise ValueError("target token id is outside the model vocabulary")
 
 
@@ -207,29 +234,28 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
     if n == 0:
         return None
     slots = lib.nmce_validate_slots(n)
-    host = torch.empty(slots, dtype=torch.int32, pin_memory=True)
+    dev_index = t.device.index if t.device.index is not None else torch.cuda.current_device()
+    host, event = _check_slot(dev_index, slots)
     if not on_side_stream:
         # On the loss stream, ahead of a kernel that fills every compute unit
         # for its whole run (the one-pass forward), so that the host's wait
         # ends early instead of after that kernel.
         _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
                 vocab_size, host.data_ptr(), _lib.stream_handle(t.device))
-        event = torch.cuda.Event()
-        if t.device.index is None or t.device.index == torch.cuda.current_device():
+        if dev_index == torch.cuda.current_device():
             event.record()  # the current device's current stream
         else:
             event.record(torch.cuda.current_stream(t.device))
-        return _PendingCheck(host, event)
+        return _PendingCheck(dev_index, host, event, slots)
     main = torch.cuda.current_stream(t.device)
     side = _side_stream(t.device)
     side.wait_stream(main)  # the targets are complete in the current stream's order
     with torch.cuda.stream(side):
         _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
                 vocab_size, host.data_ptr(), side.cuda_stream)
-        event = torch.cuda.Event()
         event.record(side)
     t.record_stream(side)  # keep the targets' memory until the side stream is done
-    return _PendingCheck(host, event)
+    return _PendingCheck(dev_index, host, event, slots)
 
 
 def validate_targets(target: torch.Tensor, vocab_size: int) -> None:
