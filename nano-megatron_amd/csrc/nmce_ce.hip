@@ -388,25 +388,31 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
 }
 
 // Forward and backward of whole-vocabulary rows (TP = 1) in one read of the
-// logits. Each workgroup walks rows blockIdx.x, + gridDim.x, ... and holds a
-// row in registers (at most kVec vectors per lane; rows 16-byte aligned, V a
-// whole number of vectors). It folds the row into (max, sum - 1) in
-// ce_stats_kernel's order, merges exactly as ce_stats_kernel does, writes the
-// loss and the statistics, then writes the gradient for the upstream value
-// usable_hint(expect[0]) of the mean (that value / gdiv per token) with
-// ce_bwd_flat_kernel's arithmetic, from the registers; the value used goes to
-// assumed[0]. Every output is bit-identical to nmce_ce_fwd followed by
-// nmce_ce_bwd_scaled with that upstream value; the backward runs only when the
-// real value differs.
+// logits. A workgroup takes row blockIdx.x (then + gridDim.x, ... when the
+// grid is capped) and holds it in registers (at most kVec vectors per lane;
+// rows 16-byte aligned, V a whole number of vectors). It folds the row into
+// (max, sum - 1) in ce_stats_kernel's order, merges exactly as
+// ce_stats_kernel does, writes the loss and the statistics, then writes the
+// gradient for the upstream value usable_hint(expect[0]) of the mean (that
+// value / gdiv per token) with ce_bwd_flat_kernel's arithmetic, from the
+// registers; the value used goes to assumed[0]. Every output is bit-identical
+// to nmce_ce_fwd followed by nmce_ce_bwd_scaled with that upstream value; the
+// backward runs only when the real value differs.
 //
-// The loads of the next row are issued at the top of each row, so they stream
-// in while this row is folded, merged and written. Rows are addressed through
-// buffer resources that span exactly one row, with each lane's whole byte
-// offset in its offset register, which the hardware range-checks: a vector
-// past the row loads as 0 and its store is dropped. So no memory instruction
-// sits in a branch, the compiler can count the outstanding ones exactly, and
-// the fold waits only for its own row, not for the next row's loads or the
-// last row's stores.
+// The kernel fits 64 registers per lane, so two 1024-lane workgroups share a
+// compute unit: while one folds, merges and writes its row, the other's loads
+// stream in, and new workgroups start as rows finish, in no lockstep. (A
+// workgroup that prefetched its next row into a second register set, one per
+// compute unit, ran 4.6% slower at [16384, 50304] bf16.) Two things keep it
+// at 64: each vector slot k has its own buffer resource (base moved by k
+// slots, range shrunk to match), so all slots share one offset register; and
+// the gradient re-unpacks each vector from the packed row rather than keeping
+// the fold's unpacked floats (twice the registers) alive across the merge.
+//
+// Every lane's whole byte offset is in its offset register, which the
+// hardware range-checks: a vector past the row loads as 0 and its store is
+// dropped. So no memory instruction sits in a branch and the compiler counts
+// the outstanding ones exactly.
 //
 // One barrier per row: every wave merges the waves' pairs itself (the same
 // DPP merge on the same values, so the same bits in every wave), and the
@@ -418,7 +424,7 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
 // vector holds it, as one element after that vector: no lane tests its
 // vectors for the target.
 template <typename T, int kVec, int kBlock = kStatsBlock>
-__global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
+__global__ __launch_bounds__(kBlock, 2 * kBlock / 256) void ce_fwdbwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, float* __restrict__ loss, float* __restrict__ out_max,
     float* __restrict__ out_sum1, const float* __restrict__ expect_in,
@@ -435,27 +441,27 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int64_t nvec = V / EPV;
-  const int row_bytes = static_cast<int>(nvec * 16);
+  const int nvec = static_cast<int>(V / EPV);  // at most kVec * kBlock
+  const int row_bytes = nvec * 16;
   const float go = expect / gdiv;
-  // A resource over row r (no bytes when r is past the last row, so that
-  // every load through it reads 0 and touches no memory).
+  // Row r of base, whole (target pick and store), or from vector slot k on.
   auto rsrc = [&](const T* base, int64_t r, int64_t stride) {
-    const bool live = r < n_rows;
-    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(live ? base + r * stride : base), 0,
-                                             live ? row_bytes : 0, 0x00020000);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + r * stride), 0, row_bytes,
+                                             0x00020000);
   };
-  auto voff = [&](int k) { return static_cast<uint32_t>(tid + k * kBlock) * 16u; };
-  u32x4 cur[kVec], nxt[kVec];
-  auto load_row = [&](int64_t r, u32x4* v) {
-    const auto rs = rsrc(x, r, ld);
+  auto rsrc_k = [&](const T* base, int64_t r, int64_t stride, int k) {
+    const int rest = row_bytes - k * kBlock * 16;
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(base + r * stride + k * kBlock * EPV),
+                                             0, rest > 0 ? rest : 0, 0x00020000);
+  };
+  const uint32_t voff = static_cast<uint32_t>(tid) * 16u;
+  u32x4 cur[kVec];
+  int parity = 0;
+  for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x, parity ^= 1) {
 #pragma unroll
     for (int k = 0; k < kVec; ++k)
-      v[k] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff(k), 0, kBufNonTemporal);
-  };
-  int64_t row = blockIdx.x;
-  load_row(row, cur);
-  for (int parity = 0; row < n_rows; row += gridDim.x, parity ^= 1) {
+      cur[k] = __builtin_amdgcn_raw_buffer_load_b128(rsrc_k(x, row, ld, k), voff, 0,
+                                                     kBufNonTemporal);
     const auto rx = rsrc(x, row, ld);
     // A target outside [0, V) (the host's check reports it after the launch)
     // picks nothing, as in ce_stats_kernel. The offset stays inside the row
@@ -465,14 +471,13 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
     const bool owned = lt >= 0 && lt < V;
     const uint32_t lt_off = owned ? static_cast<uint32_t>(lt) * sizeof(T) : 0u;
     const float xt_raw = E::buf_load1(rx, lt_off);
-    load_row(row + gridDim.x, nxt);
     // ce_stats_kernel's order: vectors k and k + 1 (kBlock apart) together
     // while both exist, then the one left, if any.
     float m = kMaxFloor, a = kExact ? -1.0f : 0.0f;
     bool paired = true;
 #pragma unroll
     for (int k = 0; k < kVec; k += 2) {
-      const int64_t i0 = tid + static_cast<int64_t>(k) * kBlock;
+      const int i0 = tid + k * kBlock;
       if (paired && i0 + kBlock < nvec) {
         float f[2 * EPV];
         E::unpack(cur[k], f);
@@ -493,6 +498,10 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
       sm_m[parity][wave] = m;
       sm_s[parity][wave] = t;
     }
+    // The target logit has arrived in every wave before any wave writes the
+    // row (the barrier alone waits for LDS, not for this load). Nothing else
+    // is outstanding here, so the wait costs nothing.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     float M = lane < kWaves ? sm_m[parity][lane] : kMaxFloor;
     float T1 = lane < kWaves ? sm_s[parity][lane] : -1.0f;
@@ -504,25 +513,25 @@ __global__ __launch_bounds__(kBlock) void ce_fwdbwd_kernel(
       loss[row] = log1pf(T1) - (xt - M);
     }
     const float scale = go / (1.0f + T1);
-    const auto rg = rsrc(g, row, ldg);
 #pragma unroll
     for (int k = 0; k < kVec; ++k) {
       u32x4 out = {0u, 0u, 0u, 0u};
-      if (tid + static_cast<int64_t>(k) * kBlock < nvec) {
+      if (tid + k * kBlock < nvec) {
+        u32x4 w = cur[k];
+        asm volatile("" : "+v"(w));  // unpack again from the packed row
         float f[EPV], y[EPV];
-        E::unpack(cur[k], f);
+        E::unpack(w, f);
 #pragma unroll
         for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
         out = E::pack(y);
       }
-      __builtin_amdgcn_raw_buffer_store_b128(out, rg, voff(k), 0, kBufNonTemporal);
+      __builtin_amdgcn_raw_buffer_store_b128(out, rsrc_k(g, row, ldg, k), voff, 0,
+                                             kBufNonTemporal);
     }
     // Every lane stores; only the owner's offset is inside the row.
-    const bool mine = owned && (lt / EPV) % kBlock == tid;
-    E::buf_store1(target_grad(xt, M, T1, go), rg,
+    const bool mine = owned && (static_cast<int>(lt) / EPV) % kBlock == tid;
+    E::buf_store1(target_grad(xt, M, T1, go), rsrc(g, row, ldg),
                   mine ? static_cast<uint32_t>(lt) * sizeof(T) : static_cast<uint32_t>(row_bytes));
-#pragma unroll
-    for (int k = 0; k < kVec; ++k) cur[k] = nxt[k];
   }
 }
 
@@ -694,8 +703,8 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
 // differs from the assumed[0] the gradient was written for, every entry is
 // scaled by gout[0] / assumed[0] (each is linear in the upstream value:
 // cross_entropy.py:64). Rows as in the one-pass kernel (16-byte aligned, V a
-// whole number of vectors), walked on its grid, so that a hit costs one short
-// launch. gout[0] also goes to observed[0] for the next forward.
+// whole number of vectors), walked by two workgroups per compute unit, so that
+// a hit costs one short launch. gout[0] also goes to observed[0] for the next forward.
 template <typename T, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
 __global__ __launch_bounds__(kBlock) void ce_grad_rescale_kernel(
     T* g, int64_t n_rows, int64_t V, int64_t ldg, const float* __restrict__ gout,
@@ -898,12 +907,11 @@ unsigned rows_grid(int64_t n_rows, int per_cu) {
   return static_cast<unsigned>(n_rows < want ? n_rows : want);
 }
 
-// Workgroups of the one-pass kernel, each walking rows: two per compute unit
-// (one resident at a time where its registers allow only one; the second
-// half starts as the first finishes, measured 0.7% faster than one per unit
-// at [16384, 50304] bf16). The backward kernels that follow it (they exit
-// at once when the upstream value matches) use the same grid.
-unsigned one_pass_grid(int64_t n_rows) { return rows_grid(n_rows, 2); }
+// Workgroups of the row kernels that run after a one-pass forward (they exit
+// at once when the upstream value matches, so a small grid walking rows costs
+// one launch, where a workgroup per row would start thousands): two per
+// compute unit.
+unsigned after_one_pass_grid(int64_t n_rows) { return rows_grid(n_rows, 2); }
 
 int launch_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab_local,
                int64_t ld, int64_t ld_grad, const int64_t* target, int64_t vocab_start,
@@ -953,7 +961,8 @@ int launch_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_
   // After the one-pass forward the backward usually exits at once: a grid of
   // two row workgroups per compute unit makes that cost one launch, where
   // the flat kernel's hundreds of thousands of workgroups would each start.
-  const dim3 grid(assumed ? one_pass_grid(n_rows) : grid_for_rows(n_rows)), block(kBwdBlock);
+  const dim3 grid(assumed ? after_one_pass_grid(n_rows) : grid_for_rows(n_rows));
+  const dim3 block(kBwdBlock);
 #define NMCE_BWD_LAUNCH(T, V)                                                              \
   hipLaunchKernelGGL((ce_bwd_kernel<T, V>), grid, block, 0, st, static_cast<const T*>(logits), \
                      static_cast<T*>(grad), n_rows, vocab_local, ld, ld_grad, target,           \
@@ -973,7 +982,7 @@ void launch_fwdbwd(const void* logits, void* grad, int64_t n_rows, int64_t vocab
                    int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
                    float* g_sumexp_m1, const float* expect, float* assumed, float gout_div,
                    hipStream_t st) {
-  hipLaunchKernelGGL((ce_fwdbwd_kernel<T, kVec>), dim3(one_pass_grid(n_rows)), dim3(kStatsBlock),
+  hipLaunchKernelGGL((ce_fwdbwd_kernel<T, kVec>), dim3(grid_for_rows(n_rows)), dim3(kStatsBlock),
                      0, st, static_cast<const T*>(logits), static_cast<T*>(grad), n_rows, vocab,
                      ld, ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, gout_div);
 }
@@ -1090,7 +1099,7 @@ int nmce_ce_grad_rescale_unless(void* grad, int dtype, int64_t n_rows, int64_t v
   if (!grad || !grad_output || !assumed) return NMCE_EINVAL_PTR;
   if (reinterpret_cast<uintptr_t>(grad) % 16 || (ld_grad * es) % 16) return NMCE_EINVAL_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(one_pass_grid(n_rows)), block(kBwdBlock);
+  const dim3 grid(after_one_pass_grid(n_rows)), block(kBwdBlock);
   if (dtype == NMCE_F32)
     hipLaunchKernelGGL(ce_grad_rescale_kernel<float>, grid, block, 0, st,
                        static_cast<float*>(grad), n_rows, vocab, ld_grad, grad_output, assumed,
