@@ -735,6 +735,47 @@ def test_one_pass_is_bit_identical(dtype, shape):
         assert torch.equal(g1, g2), f"gradient differs at upstream {upstream}"
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_one_pass_slot_boundaries(dtype):
+    """The one-pass kernel (a 1024-lane workgroup per row, vector slot k of lane
+    t at vector t + 1024 k) at widths on and next to every slot boundary it
+    handles in registers: one vector, a slot short of, at and past a full
+    slot, the 4- and 8-slot instantiations' edges, and seeded widths between.
+    Odd row counts, 37 and 513 rows. Loss and gradient bit-identical to the
+    two-pass path at upstream values 1.0 (the gradient the forward wrote) and
+    0.5 (rescaled), the logits left as they were."""
+    import nmce
+    epv = 16 // torch.tensor([], dtype=dtype).element_size()
+    slot = 1024 * epv
+    widths = [epv, slot - epv, slot, slot + epv, 2 * slot + 7 * epv, 4 * slot - epv, 4 * slot,
+              4 * slot + epv, 8 * slot - epv, 8 * slot]
+    rng = np.random.default_rng(29)
+    widths += [int(w) * epv for w in rng.integers(1, 8 * 1024, size=4)]
+    ctx = nmce.ParallelContext.single()
+    for v in widths:
+        for n in (37, 513):
+            print(f"[gpu] one-pass slots {dtype} n={n} v={v}", flush=True)
+            g = torch.Generator(device=DEV).manual_seed(v + n)
+            base = (torch.randn(n, v, device=DEV, generator=g) * 2.5).to(dtype)
+            t = torch.randint(0, v, (n,), device=DEV, generator=g)
+            for upstream in (1.0, 0.5):
+                out = []
+                for one_pass in (True, False):
+                    leaf = base.detach().clone().requires_grad_(True)
+                    logits = leaf * 1.0
+                    before = logits.detach().clone()
+                    loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, inplace=False,
+                                                             one_pass=one_pass)
+                    (loss * upstream).backward()
+                    assert torch.equal(logits.detach(), before), "the logits were modified"
+                    out.append((loss.detach(), leaf.grad.detach()))
+                (l1, g1), (l2, g2) = out
+                assert torch.equal(l1, l2), (v, n, upstream, l1.item(), l2.item())
+                if dtype == torch.bfloat16:
+                    g1, g2 = g1.view(torch.int16), g2.view(torch.int16)
+                assert torch.equal(g1, g2), f"gradient differs at v={v} n={n} upstream {upstream}"
+
+
 def test_one_pass_falls_back():
     """Rows the one-pass kernel does not take run the two-pass path with the
     same results: a width that is not a whole number of vectors, a width past
