@@ -191,7 +191,7 @@ int nmce_ce_bwd_scaled_unless(const void* logits, void* grad, int dtype, int64_t
  * rewrites `grad` from the logits only when the real upstream value differs;
  * in place, nmce_ce_grad_rescale_unless.
  * Requirements: vocab a whole number of 16-byte vectors and at most
- * nmce_ce_fwd_bwd_max_vocab(dtype) (65536 bf16, 32768 fp32); logits, grad
+ * nmce_ce_fwd_bwd_max_vocab(dtype) (131072 bf16, 65536 fp32); logits, grad
  * and both row strides 16-byte aligned. No counterpart call in the reference,
  * whose forward likewise computes the softmax that its backward returns.
  */
