@@ -63,8 +63,9 @@ int nmce_version(void);
  *                      shard, else 0.0  (raw logit, not shifted)
  * The exp-sum is carried minus the maximum's own term (exactly 1), so that
  * for a confident token, whose other terms are all small, it keeps its
- * relative precision; the loss and the target column's gradient are formed
- * from it with log1p and expm1. For fp32 logits the sum is accumulated with
+ * relative precision; the loss is formed from it with log1p, and a target
+ * at the maximum gets the gradient -(sum - 1)/sum * g from it directly. For
+ * fp32 logits the sum is accumulated with
  * the terms equal to 1 kept apart (relative error a few 2^-24); bf16 rows
  * accumulate the plain sum and subtract 1 per lane (absolute error a few
  * 2^-24), which keeps the bf16 pass within its memory-bound time.
@@ -353,10 +354,11 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
  * combined across the TP group, dZ follows from P by one factor per
  * (128-row block, token), in place, and the dX rows of the chunk and its
  * share of dW are formed by libnmce's GEMM, which reads dZ^T, the weight and
- * the hidden rows as they lie (no transposed copies). Nothing of size
- * [n_rows, vocab_local] exists (a chunk's P, then dZ^T, is [vocab_local,
- * token_chunk]), and the logits are computed once: 6 * n_rows * vocab_local
- * * hidden_size flops in all.
+ * the hidden rows as they lie (no transposed copies). The one buffer that
+ * grows with both sizes is a chunk's P, then dZ^T: bf16 [vocab_local,
+ * token_chunk], the size of the bf16 logits when the chunk holds every
+ * token. The logits are computed once: 6 * n_rows * vocab_local *
+ * hidden_size flops in all.
  * Replaces model.py:192 followed by cross_entropy.py:17-65 and the matmul
  * backward of model.py:192; with a caller that assumes the right upstream
  * value, as the reference's forward computes the softmax its backward
