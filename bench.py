@@ -30,20 +30,33 @@ Workloads:
   c5            fused stress: hidden [16384,3072], weight [256000,3072] ~
                 N(0,0.05^2) with 64 rows x30, Zipf(1.1) targets
 
-Prints one JSON line. ``roofline`` covers the dominant kernel: for the
-unfused loss its algorithmic HBM bytes per launch (what the kernel must read
-and write: tokens x vocab x bytes for each pass over the logits, plus
-per-token statistics), for the fused loss the algorithmic flops of the
-statistics GEMM (2 x tokens x vocab x hidden), over its average launch time
-measured with HIP events on the launch stream during the timed steps.
-Without ``--workload`` the line is c2 (the default path: one read of the
-logits, gradient in place) with nested objects ``two_pass`` (c2 on the
-two-pass path), ``c3``, ``c1``, ``wide`` (c2's path at a 128256-entry
-vocabulary), ``fused`` (c4) and ``c5``, each with its own
-``roofline``, ``kernels_ms`` and ``cpu_baseline``. ``cpu_baseline`` is the
-torch-CPU restatement of the reference's op sequence (oracle/ce_restate.py)
-timed on this host on a bounded sample of the same workload (repeated for
-about ``--cpu-seconds`` seconds).
+Prints one JSON line, compact enough to be kept whole by a log tail. Its top
+level is c2 on the default path (one read of the logits, gradient written in
+place, as the patched model.py call site asks with ``inplace=True``). Nested
+objects, each with ``value``, ``ms_per_step``, ``roofline`` and
+``cpu_baseline``:
+  two_pass         c2 with one_pass=False (statistics pass, then the backward)
+  c2_miss          c2 with the upstream value alternating 1.0 / 0.5 each step,
+                   so every step's assumed value is wrong (a rescale pass)
+  c3, c1, wide     the other unfused workloads on the default path
+  fused            c4 on the default path (bounded token chunks)
+  fused_one_chunk  c4 with every token in one chunk (the opt-in whose P^T has
+                   the logits' size; reports its bytes)
+  fused_recompute  c4 with one_pass=False (statistics GEMM, then a backward
+                   that recomputes the logits by vocabulary chunk)
+  c4_miss          c4 default path, upstream alternating 1.0 / 0.5
+  c5               c5 on the default path
+``roofline`` covers the dominant launch: for the unfused loss its algorithmic
+HBM bytes per launch (what it must read and write), for the fused loss the
+algorithmic flops of the C entry that takes the most time per step, over its
+average launch time measured with HIP events on the launch stream.
+Unfused steps run on fresh logits: every step takes its own copy of the
+seeded slab, refilled before each batch of timed steps, outside the timed
+region. ``cpu_baseline`` is the torch-CPU restatement of the reference's op
+sequence (oracle/ce_restate.py) timed on this host on a bounded sample of
+the same workload (repeated for about ``--cpu-seconds`` seconds); variants of
+one workload share its baseline. ``--detail PATH`` writes every measured
+field (per-kernel times, the whole-step roofline) to a JSON file as well.
 """
 
 from __future__ import annotations
@@ -83,10 +96,20 @@ WORKLOADS = {
                fused=True, n=16384, h=3072, v=256000, w_std=0.05, hot_rows=64, zipf=1.1),
 }
 
-# Nested objects of the default line: (key, workload, one_pass). The unfused
+# Nested objects of the default line: key -> (workload, options). The unfused
 # ones take --steps/--warmup, the fused ones --fused-steps/--fused-warmup.
-NESTED = [("two_pass", "c2", False), ("c3", "c3", True), ("c1", "c1", True),
-          ("wide", "wide", True), ("fused", "c4", True), ("c5", "c5", True)]
+NESTED = [
+    ("two_pass", "c2", dict(one_pass=False)),
+    ("c2_miss", "c2", dict(miss=True)),
+    ("c3", "c3", dict()),
+    ("c1", "c1", dict()),
+    ("wide", "wide", dict()),
+    ("fused", "c4", dict()),
+    ("fused_one_chunk", "c4", dict(one_chunk=True)),
+    ("fused_recompute", "c4", dict(one_pass=False)),
+    ("c4_miss", "c4", dict(miss=True)),
+    ("c5", "c5", dict()),
+]
 
 
 def parse_args():
@@ -114,6 +137,13 @@ def parse_args():
                    help="fused one-pass path: tokens per chunk (default: the library's)")
     p.add_argument("--fused-two-pass", action="store_true",
                    help="fused workloads: the recomputing backward (one_pass=False)")
+    p.add_argument("--miss", action="store_true",
+                   help="alternate the upstream value 1.0 / 0.5 every step (each step's "
+                        "assumed value is wrong)")
+    p.add_argument("--slab-budget-gb", type=float, default=48.0,
+                   help="unfused: device memory for the per-step copies of the logits")
+    p.add_argument("--detail", default=None,
+                   help="also write every measured field to this JSON file")
     return p.parse_args()
 
 
@@ -224,9 +254,8 @@ def cpu_baseline(wl: dict, seconds: float) -> dict:
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{rows} tokens x full vocab {v} ({wl['dtype']} logits), torch-CPU restatement "
-                  f"of cross_entropy.py fwd+bwd, median of {reps} after 1 warmup "
-                  f"({reps * med:.1f} s); host {host_cpu_model()}, torch {torch.__version__}",
+        "sample": f"{rows} tok x V {v} {wl['dtype']}, cross_entropy.py fwd+bwd on torch-CPU, "
+                  f"median of {reps} ({reps * med:.0f} s), {host_cpu_model()}",
         "ms_per_step": med * 1e3,
     }
 
@@ -262,37 +291,33 @@ def cpu_baseline_fused(wl: dict, seconds: float, rows: int = 128) -> dict:
         "unit": "tokens/s",
         "cores": cores,
         "kind": "port",
-        "sample": f"{rows} tokens x full vocab {v}, hidden {h}: bf16 x @ W^T, torch-CPU "
-                  f"restatement of cross_entropy.py fwd+bwd on the fp32 upcast, bf16 dX/dW "
-                  f"matmuls; median of {reps} after 1 warmup ({reps * med:.1f} s); host "
-                  f"{host_cpu_model()}, torch {torch.__version__}",
+        "sample": f"{rows} tok x V {v} x H {h}: bf16 x@W^T, cross_entropy.py on fp32, bf16 "
+                  f"dX/dW, torch-CPU, median of {reps} ({reps * med:.0f} s), {host_cpu_model()}",
         "ms_per_step": med * 1e3,
     }
 
 
-def _kernel_times(step, steps: int, with_counts: bool = False):
-    """Average duration per launch of each libnmce kernel over ``steps`` more
-    steps, from HIP event pairs recorded on the launch stream around every
-    launch (nmce.cross_entropy.kernel_timeline). Event records add small gaps
-    between launches, so this region's wall time is not the step time."""
+def _kernel_times(run_steps, steps: int):
+    """Average duration per launch of each libnmce entry over ``steps`` more
+    steps (``run_steps(k)`` runs k of them), from HIP event pairs recorded on
+    the launch stream around every launch (nmce.cross_entropy.kernel_timeline).
+    Event records add small gaps between launches, so this region's wall time
+    is not the step time. Returns ({name: ms}, {name: launches})."""
     import torch
     import nmce.cross_entropy as ce_mod
 
     timeline: list = []
     ce_mod.kernel_timeline = timeline
     try:
-        for _ in range(steps):
-            step()
+        run_steps(steps)
         torch.cuda.synchronize()
     finally:
         ce_mod.kernel_timeline = None
     per: dict[str, list[float]] = {}
     for name, s_ev, e_ev in timeline:
         per.setdefault(name, []).append(s_ev.elapsed_time(e_ev))
-    avg = {k: sum(vs) / len(vs) for k, vs in per.items()}
-    if with_counts:
-        return avg, {k: len(vs) for k, vs in per.items()}
-    return avg
+    return ({k: sum(vs) / len(vs) for k, vs in per.items()},
+            {k: len(vs) for k, vs in per.items()})
 
 
 def fused_inputs(wl: dict, dev):
@@ -316,10 +341,18 @@ def fused_inputs(wl: dict, dev):
     return x, w, t
 
 
-def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
+def _upstream(i: int, miss: bool) -> float:
+    """The upstream value of step i: 1.0 (loss.backward()), or 1.0 and 0.5 in
+    turn, so that every step's forward assumed the previous step's value."""
+    return 0.5 if (miss and i % 2) else 1.0
+
+
+def run_fused(args, name: str, steps: int, warmup: int, one_pass: bool = True,
+              one_chunk: bool = False, miss: bool = False) -> dict:
     """Time the fused LM head + loss (fwd + bwd) on workload ``name``."""
     import torch
     import nmce
+    from nmce import lmhead
 
     wl = WORKLOADS[name]
     dev = torch.device("cuda:0")
@@ -329,26 +362,28 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
     ctx = nmce.ParallelContext.single()
     xp = x.requires_grad_(True)
     wp = w.requires_grad_(True)
+    token_chunk = n if one_chunk else args.token_chunk
+    chunk = token_chunk if token_chunk is not None else lmhead.default_token_chunk(n, v)
+    counter = [0]
 
-    def step():
-        xp.grad = None  # zero_grad(set_to_none=True) between steps
-        wp.grad = None
-        loss = nmce.lmhead_vocab_parallel_cross_entropy(xp, wp, t, 0, v, ctx,
-                                                        vocab_chunk=args.vocab_chunk,
-                                                        token_chunk=args.token_chunk,
-                                                        one_pass=not args.fused_two_pass)
-        loss.backward()
-        return loss
+    def run_steps(k):
+        for _ in range(k):
+            xp.grad = None  # zero_grad(set_to_none=True) between steps
+            wp.grad = None
+            loss = nmce.lmhead_vocab_parallel_cross_entropy(
+                xp, wp, t, 0, v, ctx, vocab_chunk=args.vocab_chunk, token_chunk=token_chunk,
+                one_pass=one_pass)
+            g = _upstream(counter[0], miss)
+            counter[0] += 1
+            (loss * g if miss else loss).backward()
 
-    for _ in range(warmup):
-        step()
+    run_steps(warmup)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(steps):
-        step()
+    run_steps(steps)
     torch.cuda.synchronize()
     ms_per_step = (time.perf_counter() - t0) * 1e3 / steps
-    avg_ms, counts = _kernel_times(step, steps, with_counts=True)
+    avg_ms, counts = _kernel_times(run_steps, steps)
 
     calib = None
     if args.calibrate_copy:
@@ -363,44 +398,39 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
         del dst
 
     gemm_flops = 2.0 * n * v * h   # one product over every token
-    one_pass = "nmce_lmhead_ce_fused_chunk_stats" in avg_ms
-    # The statistics GEMM: on the one-pass path one launch per token chunk
-    # (the GEMM that keeps the exponentials, plus the small reduction of its
-    # partials), else one launch over every token.
-    dominant = "nmce_lmhead_ce_fused_chunk_stats" if one_pass else "nmce_lmhead_ce_fwd_stats"
+    # Algorithmic flops per step of each C entry: the one-pass statistics call
+    # is the forward GEMM of its chunk, the gradients call the dX and dW
+    # GEMMs of its chunk; the recomputing path's statistics call is the
+    # forward GEMM and its backward call the three GEMMs of the backward
+    # (the recomputation counted as executed, not as algorithmic work).
+    entry_flops = {
+        "nmce_lmhead_ce_fused_chunk_stats": gemm_flops,
+        "nmce_lmhead_ce_fused_chunk_grads": 2 * gemm_flops,
+        "nmce_lmhead_ce_fwd_stats": gemm_flops,
+        "nmce_lmhead_ce_bwd": 3 * gemm_flops,
+    }
+    step_ms = {k: avg_ms[k] * counts[k] / steps for k in avg_ms}
+    dominant = max((k for k in entry_flops if k in avg_ms), key=lambda k: step_ms[k])
     per_step = counts[dominant] / steps
-    flops_per_launch = gemm_flops / per_step
+    flops_per_launch = entry_flops[dominant] / per_step
     achieved = flops_per_launch / (avg_ms[dominant] * 1e-3) / 1e12
     alg_flops = 3 * gemm_flops      # forward GEMM + the dX and dW GEMMs
-    # the recomputing backward also recomputes the logits
-    exe_flops = alg_flops if one_pass else 4 * gemm_flops
+    on_one_pass = "nmce_lmhead_ce_fused_chunk_stats" in avg_ms
+    exe_flops = alg_flops if on_one_pass else 4 * gemm_flops
+    vpad = (v + 255) // 256 * 256
+    pt_bytes = vpad * ((min(chunk, n) + 63) // 64 * 64) * 2 if on_one_pass else None
+    path = (("one pass, one chunk of every token" if one_chunk else
+             f"one pass, chunks of {min(chunk, n)} tokens") if on_one_pass else
+            "recomputing backward")
     result = {
         "metric": METRIC,
         "value": n / (ms_per_step * 1e-3),
         "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
         "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic",
         "config": {
-            "workload": f"{name}: {wl['desc']}",
-            "tokens": n,
-            "hidden": h,
-            "vocab_local": v,
-            "tp": 1,
-            "path": ("nmce.lmhead_vocab_parallel_cross_entropy fwd+bwd, one pass: per chunk "
-                     "of tokens the statistics GEMM keeps its exponentials, dZ follows from "
-                     "them, dX and dW by libnmce's GEMM (logits computed once, never stored "
-                     "whole; bf16 MFMA, fp32 accumulate), target validation"
-                     if one_pass else
-                     "nmce.lmhead_vocab_parallel_cross_entropy fwd+bwd (logits never stored; "
-                     "recomputed by vocabulary chunk in the backward; bf16 MFMA, fp32 "
-                     "accumulate), target validation, dX and dW"),
+            "workload": name,
+            "path": path + (", upstream 1/0.5 alternating" if miss else ""),
+            "pt_bytes": pt_bytes,
         },
         "roofline": {
             "bound": "mfma",
@@ -409,27 +439,27 @@ def run_fused(args, name: str, steps: int, warmup: int, with_cpu: bool) -> dict:
             "peak": MFMA_BF16_PEAK_TFLOPS,
             "unit": "TFLOP/s",
             "frac": achieved / MFMA_BF16_PEAK_TFLOPS,
-            "traffic": (measured_traffic(name, "lmhead_p_kernel", LMHEAD_TRAFFIC_FILE)
-                        if one_pass else None),
-            "alg_flops_per_launch": flops_per_launch,
-            "avg_launch_ms": avg_ms[dominant],
-            "launches_per_step": per_step,
+            "traffic": measured_traffic(f"{name}:{min(chunk, n)}", dominant,
+                                        LMHEAD_TRAFFIC_FILE) if on_one_pass else None,
         },
+        "step_frac": alg_flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
+    }
+    detail = {
         "kernels_ms": avg_ms,
-        "path_roofline": {
-            "alg_flops_per_step": alg_flops,
-            "executed_flops_per_step": exe_flops,
-            "frac_alg_wall": alg_flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-            "frac_executed_wall": exe_flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
-        },
+        "launches_per_step": {k: c / steps for k, c in counts.items()},
+        "alg_flops_per_launch": flops_per_launch,
+        "alg_flops_per_step": alg_flops,
+        "executed_flops_per_step": exe_flops,
+        "frac_executed_wall": exe_flops / (ms_per_step * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS,
         "device": torch.cuda.get_device_name(0),
+        "steps": steps,
+        "warmup": warmup,
     }
     if calib is not None:
-        result["calibration_copy_bytes"] = calib
+        detail["calibration_copy_bytes"] = calib
     del x, w, t, xp, wp
     torch.cuda.empty_cache()
-    result["cpu_baseline"] = cpu_baseline_fused(wl, args.cpu_seconds) if with_cpu else None
-    return result
+    return result, detail
 
 
 def unfused_alg_bytes(n: int, slab: int) -> dict:
@@ -445,12 +475,15 @@ def unfused_alg_bytes(n: int, slab: int) -> dict:
         # one-pass forward + backward: the logits read once, the gradient
         # written once (in place or to a new buffer)
         "nmce_ce_fwd_bwd": 2 * slab + 20 * n,
+        # a miss after an in-place one-pass forward: the gradient read and
+        # written once more
+        "nmce_ce_grad_rescale_unless": 2 * slab,
         "nmce_ce_combine": 24 * n,
     }
 
 
-def run_unfused(args, name: str, one_pass: bool, steps: int, warmup: int,
-                with_cpu: bool) -> dict:
+def run_unfused(args, name: str, steps: int, warmup: int, one_pass: bool = True,
+                miss: bool = False) -> dict:
     """Time the drop-in loss (fwd + bwd) on unfused workload ``name``."""
     import torch
     import nmce
@@ -466,7 +499,7 @@ def run_unfused(args, name: str, one_pass: bool, steps: int, warmup: int,
     start, end = rank * v, (rank + 1) * v
 
     gen = torch.Generator(device=dev).manual_seed(0)
-    base = (torch.randn(n, v, device=dev, generator=gen) * wl["sigma"]).to(dt)
+    pristine = (torch.randn(n, v, device=dev, generator=gen) * wl["sigma"]).to(dt)
     target = torch.randint(0, v * tp, (wl["b"], wl["s"]), device=dev, generator=gen)
     ctx = nmce.ParallelContext(rank=rank, world_size=tp, tp_size=tp, tp_rank=rank, pp_size=1,
                                pp_rank=0, dp_size=1, dp_rank=0)
@@ -489,79 +522,79 @@ def run_unfused(args, name: str, one_pass: bool, steps: int, warmup: int,
 
         ce_mod._exchange_stats = emulated_all_gather
 
-    # Non-leaf logits produced by an LM-head node, as at model.py:277: the
-    # gradient goes in place into the logits storage (by the one-pass forward
-    # at TP = 1, by the backward otherwise).
+    # Every step runs on its own copy of the seeded logits (the loss writes
+    # the gradient into them): as many copies as the budget holds, refilled
+    # from the pristine slab before each batch of steps, outside the timed
+    # region.
+    slab_bytes = n * v * esize
+    nbuf = int(max(1, min(steps, args.slab_budget_gb * 1e9 // slab_bytes)))
+    bufs = [torch.empty_like(pristine) for _ in range(nbuf)]
+
+    # Non-leaf logits produced by an LM-head node, as at model.py:277; the
+    # call site asks for the gradient in place (inplace=True), as the patched
+    # model.py does: the one-pass forward writes it into the logits.
     anchor = torch.zeros((), device=dev, requires_grad=True)
     lm_head = lm_head_stand_in()
-    slab = base.view(wl["b"], wl["s"], v)
+    counter = [0]
 
-    def step():
-        logits = lm_head.apply(slab, anchor)
+    def one_step(buf):
+        logits = lm_head.apply(buf.view(wl["b"], wl["s"], v), anchor)
         loss = nmce.vocab_parallel_cross_entropy(logits, target, start, end, ctx,
-                                                 one_pass=one_pass)
-        loss.backward()
-        return loss
+                                                 one_pass=one_pass, inplace=True)
+        g = _upstream(counter[0], miss)
+        counter[0] += 1
+        (loss * g if miss else loss).backward()
+
+    def run_batches(k, timed):
+        """k steps in batches of nbuf fresh copies; returns the summed wall time
+        of the batches (each bracketed by synchronize)."""
+        total = 0.0
+        done = 0
+        while done < k:
+            m = min(nbuf, k - done)
+            for b in bufs[:m]:
+                b.copy_(pristine)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for b in bufs[:m]:
+                one_step(b)
+            torch.cuda.synchronize()
+            total += time.perf_counter() - t0
+            done += m
+        return total
 
     try:
-        for _ in range(warmup):
-            step()
-        torch.cuda.synchronize()
-
-        # Timed region: K steps as a user runs them, nothing added.
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            step()
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        ms_per_step = (t1 - t0) * 1e3 / steps
-        avg_ms = _kernel_times(step, steps)
+        run_batches(warmup, False)
+        # Timed region: K steps as a user runs them, on fresh logits.
+        ms_per_step = run_batches(steps, True) * 1e3 / steps
+        avg_ms, counts = _kernel_times(lambda k: run_batches(k, False), steps)
     finally:
         ce_mod._exchange_stats = saved_exchange
 
-    slab_bytes = n * v * esize
     alg = unfused_alg_bytes(n, slab_bytes)
-    dominant = max((k for k in alg if k in avg_ms), key=lambda k: avg_ms[k])
+    step_ms = {k: avg_ms[k] * counts[k] / steps for k in avg_ms}
+    dominant = max((k for k in alg if k in avg_ms), key=lambda k: step_ms[k])
     achieved = alg[dominant] / (avg_ms[dominant] * 1e-3) / 1e9
     # The graded step figure: a forward pass over the logits and a backward
     # pass that reads them again and writes the gradient (the upstream value
     # is known only in the backward): 3 V b + 28 bytes per token.
     step_bytes = 3 * slab_bytes + n * 28
-    kernel_ms = sum(avg_ms.values())
+    kernel_ms = sum(step_ms.values())
     on_one_pass = "nmce_ce_fwd_bwd" in avg_ms
     # What this path's step must move: the one-pass path reads the logits once
     # and writes the gradient once (2 V b + 28 per token: target, statistics,
     # loss); the two-pass path 3 V b + 28.
     path_bytes = 2 * slab_bytes + n * 28 if on_one_pass else step_bytes
-    traffic_key = {"nmce_ce_bwd_scaled": "nmce_ce_bwd"}.get(dominant, dominant)
-    if dominant == "nmce_ce_fwd_bwd":
-        traffic_key = "nmce_ce_fwd_bwd_inplace"
+    traffic_key = {"nmce_ce_bwd_scaled": "nmce_ce_bwd",
+                   "nmce_ce_fwd_bwd": "nmce_ce_fwd_bwd_inplace"}.get(dominant, dominant)
+    path = "one pass, in place" if on_one_pass else "two passes, in place"
     result = {
         "metric": METRIC,
         "value": n / (ms_per_step * 1e-3),
         "unit": "tokens/s",
-        "n_gpus": 1,
-        "steps": steps,
-        "warmup": warmup,
         "ms_per_step": ms_per_step,
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "f32",
-        "data": "synthetic",
-        "config": {
-            "workload": f"{name}: {wl['desc']}",
-            "tokens": n,
-            "vocab_local": v,
-            "tp": tp,
-            "tp_rank": rank,
-            "logits_dtype": wl["dtype"],
-            "path": ("nmce.vocab_parallel_cross_entropy fwd+bwd, target validation; the "
-                     "one-pass kernel (logits read once, gradient written in place by the "
-                     "forward)" if on_one_pass else
-                     "nmce.vocab_parallel_cross_entropy fwd+bwd, two passes (statistics, then "
-                     "the in-place gradient), target validation"),
-        },
+        "config": {"workload": name,
+                   "path": path + (", upstream 1/0.5 alternating" if miss else "")},
         "roofline": {
             "bound": "hbm",
             "kernel": dominant,
@@ -570,46 +603,46 @@ def run_unfused(args, name: str, one_pass: bool, steps: int, warmup: int,
             "unit": "GB/s",
             "frac": achieved / HBM_PEAK_GBS,
             "traffic": measured_traffic(name, traffic_key),
-            "alg_bytes_per_launch": alg[dominant],
-            "avg_launch_ms": avg_ms[dominant],
         },
+        "step_frac": path_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+    }
+    detail = {
         "kernels_ms": avg_ms,
-        "path_roofline": {
-            "alg_bytes_per_step": path_bytes,
-            "kernel_ms_per_step": kernel_ms,
-            "frac_kernels": path_bytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
-            "frac_wall": path_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        },
+        "launches_per_step": {k: c / steps for k, c in counts.items()},
+        "alg_bytes_per_launch": alg[dominant],
+        "path_bytes_per_step": path_bytes,
+        "kernel_ms_per_step": kernel_ms,
+        "frac_kernels": path_bytes / (kernel_ms * 1e-3) / 1e9 / HBM_PEAK_GBS,
+        "fresh_copies": nbuf,
         "device": torch.cuda.get_device_name(0),
+        "steps": steps,
+        "warmup": warmup,
     }
     if on_one_pass:
-        # The whole step credited with the two passes' bytes: a comparison
-        # with the two-pass design, not a roofline fraction.
-        result["path_roofline"]["two_pass_equivalent"] = {
+        # The step and the kernel credited with the two passes' bytes (what
+        # the two-pass path must move): a comparison, not a roofline fraction.
+        detail["two_pass_equivalent"] = {
             "alg_bytes_per_step": step_bytes,
             "ratio_to_peak_wall": step_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
-        }
-        # The same kernel credited with the two passes' bytes (3 V b + 28 per
-        # token, what the two-pass path must move): how it compares with the
-        # graded figure, not a roofline fraction.
-        two = step_bytes
-        result["roofline"]["two_pass_equivalent"] = {
-            "alg_bytes_per_launch": two,
-            "achieved": two / (avg_ms[dominant] * 1e-3) / 1e9,
-            "ratio_to_peak": two / (avg_ms[dominant] * 1e-3) / 1e9 / HBM_PEAK_GBS,
+            "kernel_ratio_to_peak": step_bytes / (avg_ms[dominant] * 1e-3) / 1e9 / HBM_PEAK_GBS,
         }
     if args.calibrate_copy:
         from nmce import _lib as L
-        dst = torch.empty_like(base)
-        L.check(L.load().nmce_stream_copy(base.data_ptr(), dst.data_ptr(), slab_bytes,
+        dst = torch.empty_like(pristine)
+        L.check(L.load().nmce_stream_copy(pristine.data_ptr(), dst.data_ptr(), slab_bytes,
                                           L.stream_handle(dev)), "nmce_stream_copy")
         torch.cuda.synchronize()
-        result["calibration_copy_bytes"] = slab_bytes
+        detail["calibration_copy_bytes"] = slab_bytes
         del dst
-    del base, slab
+    del pristine, bufs
     torch.cuda.empty_cache()
-    result["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds) if with_cpu else None
-    return result
+    return result, detail
+
+
+def _short_cpu(cb: dict | None) -> dict | None:
+    if cb is None:
+        return None
+    return {k: cb[k] for k in ("value", "unit", "cores", "kind", "sample")}
 
 
 def main() -> int:
@@ -621,36 +654,93 @@ def main() -> int:
         return 2
 
     with_cpu = not args.no_cpu_baseline
+    details = {}
     if args.workload is not None:
         wl = WORKLOADS[args.workload]
         if wl.get("fused"):
-            result = run_fused(args, args.workload, args.steps, args.warmup, with_cpu)
+            result, det = run_fused(args, args.workload, args.steps, args.warmup,
+                                    one_pass=not args.fused_two_pass, miss=args.miss)
+            cpu = cpu_baseline_fused(wl, args.cpu_seconds) if with_cpu else None
         else:
-            result = run_unfused(args, args.workload, not args.two_pass, args.steps,
-                                 args.warmup, with_cpu)
-        print(json.dumps(result), flush=True)
-        return 0
-
-    # Default: c2 on the default path, every other config nested. Every GPU
-    # measurement runs before the first CPU baseline, whose worker threads
-    # would otherwise compete with the launching thread.
-    result = run_unfused(args, "c2", True, args.steps, args.warmup, False)
-    for key, name, one_pass in NESTED:
-        print(f"[bench] {key}: {name}", file=sys.stderr, flush=True)
-        if WORKLOADS[name].get("fused"):
-            result[key] = run_fused(args, name, args.fused_steps, args.fused_warmup, False)
+            result, det = run_unfused(args, args.workload, args.steps, args.warmup,
+                                      one_pass=not args.two_pass, miss=args.miss)
+            cpu = cpu_baseline(wl, args.cpu_seconds) if with_cpu else None
+        result["cpu_baseline"] = _short_cpu(cpu)
+        details[args.workload] = det
+        out = _headline(result, args.steps, args.warmup, wl)
+    else:
+        # Default: c2 on the default path, every other config nested. Every
+        # GPU measurement runs before the first CPU baseline, whose worker
+        # threads would otherwise compete with the launching thread.
+        result, details["c2"] = run_unfused(args, "c2", args.steps, args.warmup)
+        out = _headline(result, args.steps, args.warmup, WORKLOADS["c2"])
+        for key, name, opts in NESTED:
+            print(f"[bench] {key}: {name} {opts}", file=sys.stderr, flush=True)
+            if WORKLOADS[name].get("fused"):
+                out[key], details[key] = run_fused(args, name, args.fused_steps,
+                                                   args.fused_warmup, **opts)
+            else:
+                out[key], details[key] = run_unfused(args, name, args.steps, args.warmup,
+                                                     **opts)
+            out[key].pop("metric")
+            out[key].pop("unit")
+        if with_cpu:
+            print("[bench] CPU baselines", file=sys.stderr, flush=True)
+            cpu = {"c2": cpu_baseline(WORKLOADS["c2"], args.cpu_seconds)}
+            out["cpu_baseline"] = _short_cpu(cpu["c2"])
+            for key, name, _ in NESTED:
+                if name not in cpu:
+                    wl = WORKLOADS[name]
+                    cpu[name] = (cpu_baseline_fused(wl, args.cpu_seconds) if wl.get("fused")
+                                 else cpu_baseline(wl, args.cpu_seconds))
+                out[key]["cpu_baseline"] = _short_cpu(cpu[name])
         else:
-            result[key] = run_unfused(args, name, one_pass, args.steps, args.warmup, False)
-    if with_cpu:
-        print("[bench] CPU baselines", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(WORKLOADS["c2"], args.cpu_seconds)
-        for key, name, _ in NESTED:
-            wl = WORKLOADS[name]
-            result[key]["cpu_baseline"] = (cpu_baseline_fused(wl, args.cpu_seconds)
-                                           if wl.get("fused") else
-                                           cpu_baseline(wl, args.cpu_seconds))
-    print(json.dumps(result), flush=True)
+            out["cpu_baseline"] = None
+            for key, _, _ in NESTED:
+                out[key]["cpu_baseline"] = None
+    if args.detail:
+        pathlib.Path(args.detail).write_text(json.dumps(details, indent=1))
+    print(json.dumps(_round(out), separators=(",", ":")), flush=True)
     return 0
+
+
+def _headline(result: dict, steps: int, warmup: int, wl: dict) -> dict:
+    """The contract's top-level fields around one workload's result."""
+    fused = bool(wl.get("fused"))
+    out = {
+        "metric": METRIC,
+        "value": result["value"],
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": result["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if not fused else "bf16",
+        "data": "synthetic",
+        "config": dict(result["config"], workload=wl["desc"]),
+        "roofline": result["roofline"],
+        "step_frac": result["step_frac"],
+    }
+    if not fused:
+        out["config"]["logits_dtype"] = wl["dtype"]
+    if "cpu_baseline" in result:
+        out["cpu_baseline"] = result["cpu_baseline"]
+    return out
+
+
+def _round(obj):
+    """Floats to 4 significant digits (a shorter line; no figure is quoted to
+    more)."""
+    if isinstance(obj, float):
+        return float(f"{obj:.4g}")
+    if isinstance(obj, dict):
+        return {k: _round(v) for k, v in obj.items()}
+    if isinstance(obj, list):
+        return [_round(v) for v in obj]
+    return obj
 
 
 if __name__ == "__main__":

@@ -126,6 +126,19 @@ int nmce_validate_targets(const int64_t* target, int64_t n_rows,
                           void* stream);
 
 /*
+ * The same check (cross_entropy.py:79-81) in one workgroup, for a loss
+ * kernel that follows on the same stream and must leave its inputs untouched
+ * on a bad target (the reference raises before touching anything, :80-81):
+ * the number of bad targets, saturated at INT32_MAX, goes to bad_count[0]
+ * (for the host; device or pinned host memory) and to bad_flag[0] (device
+ * memory, passed to nmce_ce_fwd_bwd as target_bad). Both are written
+ * unconditionally, so neither needs clearing.
+ */
+int nmce_validate_targets_once(const int64_t* target, int64_t n_rows,
+                               int64_t vocab_total, int32_t* bad_count,
+                               int32_t* bad_flag, void* stream);
+
+/*
  * Backward over one shard: grad = (softmax - onehot(target)) * grad_output.
  * Replaces cross_entropy.py:53-65 plus the autograd cast back to the logits
  * dtype (the .float() at :83).
@@ -195,12 +208,16 @@ int nmce_ce_bwd_scaled_unless(const void* logits, void* grad, int dtype, int64_t
  * nmce_ce_fwd_bwd_max_vocab(dtype) (131072 bf16, 65536 fp32); logits, grad
  * and both row strides 16-byte aligned. No counterpart call in the reference,
  * whose forward likewise computes the softmax that its backward returns.
+ * target_bad (may be NULL): the bad_flag of nmce_validate_targets_once,
+ * enqueued before on the same stream. When it is nonzero the kernel writes
+ * nothing at all, so logits that were to receive their gradient in place
+ * are left as they were.
  */
 int64_t nmce_ce_fwd_bwd_max_vocab(int dtype);
 int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab,
                     int64_t ld, int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
                     float* g_sumexp_m1, const float* grad_expected, float* grad_assumed,
-                    float gout_div, void* stream);
+                    const int32_t* target_bad, float gout_div, void* stream);
 
 /*
  * Backward after an in-place nmce_ce_fwd_bwd (grad == logits), whose
@@ -366,15 +383,18 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
  * --------------------------------------------------------------------------- */
 
 /*
- * Workspace layout (int64 values) written to layout[0 .. 8]:
+ * Workspace layout (int64 values) written to layout[0 .. 10]:
  *   [0] total bytes  [1] chunk (tokens per chunk)  [2] n_chunks
  *   [3] ldt (chunk padded to 64)  [4] vpad (vocab_local padded to 256)
- *   [5] nb (ceil(vocab_local / 128))  [6..8] byte offsets of P^T
+ *   [5] nb (ceil(vocab_local / 128))  [6..9] byte offsets of P^T
  *   (= dZ_c^T, [vpad, ldt]: the only chunk-sized buffer; both backward
- *   products read it, hidden and weight as they lie), the partial statistics
- *   and the fp32 dW accumulator (present when n_chunks > 1).
+ *   products read it, hidden and weight as they lie), the partial statistics,
+ *   the fp32 dW accumulator (present when n_chunks > 1) and the fp32 partials
+ *   of a chunk's dX product when it is split over K  [10] the number of K
+ *   ranges of that product (1: not split; more when a chunk's dX has too few
+ *   256x256 tiles to fill the current device's compute units).
  */
-#define NMCE_LMHEAD_FUSED_LAYOUT_FIELDS 9
+#define NMCE_LMHEAD_FUSED_LAYOUT_FIELDS 11
 int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
                                 int64_t token_chunk, int64_t* layout);
 

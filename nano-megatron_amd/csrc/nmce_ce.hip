@@ -245,6 +245,39 @@ __global__ __launch_bounds__(kValidateThreads) void validate_targets_kernel(
   }
 }
 
+// The same check over every row in one workgroup, for a loss kernel that
+// follows on the same stream and must not write anything when a target is
+// bad: the count of bad targets (saturated at INT32_MAX) goes to bad_count
+// (pinned host memory, for the host's ValueError) and to bad_flag (device
+// memory, which the one-pass kernels read before their first store). One
+// workgroup writes both unconditionally, so neither needs clearing and a
+// captured graph replays it as it is.
+constexpr int kCheckOnceThreads = 1024;
+
+__global__ __launch_bounds__(kCheckOnceThreads) void validate_targets_once_kernel(
+    const int64_t* __restrict__ target, int64_t n_rows, int64_t vocab_total,
+    int32_t* __restrict__ bad_count, int32_t* __restrict__ bad_flag) {
+  __shared__ int64_t sm_bad[kCheckOnceThreads / 64];
+  int64_t bad = 0;
+#pragma unroll 8
+  for (int64_t r = threadIdx.x; r < n_rows; r += kCheckOnceThreads) {
+    const int64_t tg = target[r];
+    bad += (tg < 0 || tg >= vocab_total) ? 1 : 0;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) bad += __shfl_xor(bad, off);
+  if ((threadIdx.x & 63) == 0) sm_bad[threadIdx.x >> 6] = bad;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int64_t total = 0;
+#pragma unroll
+    for (int w = 0; w < kCheckOnceThreads / 64; ++w) total += sm_bad[w];
+    const int32_t c = total > INT32_MAX ? INT32_MAX : static_cast<int32_t>(total);
+    bad_count[0] = c;
+    bad_flag[0] = c;
+  }
+}
+
 
 // Replace y[d] by the target column's gradient when 0 <= d < K, with px the
 // vector's first logit. The target's logit is read again from px[d] (the
@@ -423,17 +456,23 @@ __global__ __launch_bounds__(kBlock) void ce_bwd_flat_kernel(
 // overwritten by its gradient. The target column is written by the lane whose
 // vector holds it, as one element after that vector: no lane tests its
 // vectors for the target.
+//
+// With bad_flag (the count validate_targets_once_kernel wrote just before, on
+// the same stream) nonzero, every workgroup leaves at once: no output is
+// written, so logits that were to be overwritten by their gradient stay as
+// they were when the host raises for the bad target.
 template <typename T, int kVec, int kBlock = kStatsBlock>
 __global__ __launch_bounds__(kBlock, 2 * kBlock / 256) void ce_fwdbwd_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, float* __restrict__ loss, float* __restrict__ out_max,
     float* __restrict__ out_sum1, const float* __restrict__ expect_in,
-    float* __restrict__ assumed, float gdiv) {
+    float* __restrict__ assumed, const int32_t* __restrict__ bad_flag, float gdiv) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
   constexpr int kWaves = kBlock / 64;
   constexpr bool kExact = sizeof(T) == 4;
   static_assert(kVec % 2 == 0, "vectors are folded in pairs");
+  if (bad_flag && bad_flag[0] != 0) return;
   const float expect = usable_hint(expect_in[0]);
   if (blockIdx.x == 0 && threadIdx.x == 0) assumed[0] = expect;
   __shared__ float sm_m[2][kWaves];
@@ -543,10 +582,15 @@ __global__ __launch_bounds__(kBlock, 2 * kBlock / 256) void ce_fwdbwd_kernel(
 // for its gradient, while the register part's gradient is written, and the
 // next row's register part is loaded right after this row's fold. Same fold
 // order, merges and per-element arithmetic as ce_fwdbwd_kernel (and so as
-// ce_stats_kernel and ce_bwd_flat_kernel): bit-identical outputs.
+// ce_stats_kernel and ce_bwd_flat_kernel): bit-identical outputs. A nonzero
+// bad_flag stops it before any store, as in ce_fwdbwd_kernel.
 constexpr int kWideLo = 7;
 constexpr int kWideHi = 9;
 constexpr int kWideLdsBytes = kWideHi * kStatsBlock * 16;  // 144 KiB
+// The dynamic part plus the kernel's static pairs (two floats per wave) must
+// fit gfx950's 160 KiB of LDS per compute unit.
+static_assert(kWideLdsBytes + 2 * (kStatsBlock / 64) * 4 <= 160 * 1024,
+              "the wide-row kernel's LDS exceeds a compute unit's 160 KiB");
 
 typedef __attribute__((address_space(3))) void lds_void_t;
 
@@ -555,7 +599,7 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
     const T* x, T* g, int64_t n_rows, int64_t V, int64_t ld, int64_t ldg,
     const int64_t* __restrict__ target, float* __restrict__ loss, float* __restrict__ out_max,
     float* __restrict__ out_sum1, const float* __restrict__ expect_in,
-    float* __restrict__ assumed, float gdiv) {
+    float* __restrict__ assumed, const int32_t* __restrict__ bad_flag, float gdiv) {
   using E = Elem<T>;
   constexpr int EPV = E::kPerVec;
   constexpr int kBlock = kStatsBlock;
@@ -563,6 +607,7 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
   constexpr bool kExact = sizeof(T) == 4;
   extern __shared__ __align__(16) char lds_dyn[];
   u32x4* hi = reinterpret_cast<u32x4*>(lds_dyn);  // vector kWideLo + k of lane t: hi[k * kBlock + t]
+  if (bad_flag && bad_flag[0] != 0) return;
   const float expect = usable_hint(expect_in[0]);
   if (blockIdx.x == 0 && threadIdx.x == 0) assumed[0] = expect;
   __shared__ float sm_m[kWaves];
@@ -872,6 +917,17 @@ int nmce_validate_targets(const int64_t* target, int64_t n_rows, int64_t vocab_t
   return launch_status();
 }
 
+int nmce_validate_targets_once(const int64_t* target, int64_t n_rows, int64_t vocab_total,
+                               int32_t* bad_count, int32_t* bad_flag, void* stream) {
+  if (n_rows < 0 || vocab_total < 1) return NMCE_EINVAL_SHAPE;
+  if (n_rows == 0) return NMCE_OK;
+  if (!target || !bad_count || !bad_flag) return NMCE_EINVAL_PTR;
+  hipLaunchKernelGGL(validate_targets_once_kernel, dim3(1), dim3(kCheckOnceThreads), 0,
+                     static_cast<hipStream_t>(stream), target, n_rows, vocab_total, bad_count,
+                     bad_flag);
+  return launch_status();
+}
+
 int nmce_ce_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab_local,
                 int64_t ld, int64_t ld_grad, const int64_t* target, int64_t vocab_start,
                 const float* g_max, const float* g_sumexp_m1, const float* grad_output,
@@ -980,18 +1036,19 @@ int launch_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_
 template <typename T, int kVec>
 void launch_fwdbwd(const void* logits, void* grad, int64_t n_rows, int64_t vocab, int64_t ld,
                    int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
-                   float* g_sumexp_m1, const float* expect, float* assumed, float gout_div,
-                   hipStream_t st) {
+                   float* g_sumexp_m1, const float* expect, float* assumed,
+                   const int32_t* bad_flag, float gout_div, hipStream_t st) {
   hipLaunchKernelGGL((ce_fwdbwd_kernel<T, kVec>), dim3(grid_for_rows(n_rows)), dim3(kStatsBlock),
                      0, st, static_cast<const T*>(logits), static_cast<T*>(grad), n_rows, vocab,
-                     ld, ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, gout_div);
+                     ld, ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, bad_flag,
+                     gout_div);
 }
-// One workgroup per compute unit (the LDS part of a row takes 128 KiB).
+// One workgroup per compute unit (the LDS part of a row takes 144 KiB).
 template <typename T>
 int launch_fwdbwd_wide(const void* logits, void* grad, int64_t n_rows, int64_t vocab, int64_t ld,
                        int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
-                       float* g_sumexp_m1, const float* expect, float* assumed, float gout_div,
-                       hipStream_t st) {
+                       float* g_sumexp_m1, const float* expect, float* assumed,
+                       const int32_t* bad_flag, float gout_div, hipStream_t st) {
   static bool lds_ok = false;  // the attribute is set once per process and kernel
   if (!lds_ok) {
     const hipError_t e =
@@ -1003,7 +1060,8 @@ int launch_fwdbwd_wide(const void* logits, void* grad, int64_t n_rows, int64_t v
   const unsigned grid = rows_grid(n_rows, 1);
   hipLaunchKernelGGL((ce_fwdbwd_wide_kernel<T>), dim3(grid), dim3(kStatsBlock), kWideLdsBytes, st,
                      static_cast<const T*>(logits), static_cast<T*>(grad), n_rows, vocab, ld,
-                     ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, gout_div);
+                     ld_grad, target, loss, g_max, g_sumexp_m1, expect, assumed, bad_flag,
+                     gout_div);
   return NMCE_OK;
 }
 }  // namespace
@@ -1039,7 +1097,7 @@ int64_t nmce_ce_fwd_bwd_max_vocab(int dtype) {
 int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, int64_t vocab,
                     int64_t ld, int64_t ld_grad, const int64_t* target, float* loss, float* g_max,
                     float* g_sumexp_m1, const float* grad_expected, float* grad_assumed,
-                    float gout_div, void* stream) {
+                    const int32_t* target_bad, float gout_div, void* stream) {
   if (dtype != NMCE_F32 && dtype != NMCE_BF16) return NMCE_EINVAL_DTYPE;
   const int64_t es = dtype == NMCE_F32 ? 4 : 2;
   const int64_t epv = 16 / es;
@@ -1060,10 +1118,10 @@ int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, i
     const int rc = dtype == NMCE_F32
                        ? launch_fwdbwd_wide<float>(logits, grad, n_rows, vocab, ld, ld_grad, target,
                                                    loss, g_max, g_sumexp_m1, grad_expected,
-                                                   grad_assumed, gout_div, st)
+                                                   grad_assumed, target_bad, gout_div, st)
                        : launch_fwdbwd_wide<uint16_t>(logits, grad, n_rows, vocab, ld, ld_grad,
                                                       target, loss, g_max, g_sumexp_m1,
-                                                      grad_expected, grad_assumed, gout_div, st);
+                                                      grad_expected, grad_assumed, target_bad, gout_div, st);
     return rc != NMCE_OK ? rc : launch_status();
   }
   const bool small = per_lane <= kOnePassVecs[0];
@@ -1071,20 +1129,20 @@ int nmce_ce_fwd_bwd(const void* logits, void* grad, int dtype, int64_t n_rows, i
     if (small)
       launch_fwdbwd<float, kOnePassVecs[0]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
                                             loss, g_max, g_sumexp_m1, grad_expected, grad_assumed,
-                                            gout_div, st);
+                                            target_bad, gout_div, st);
     else
       launch_fwdbwd<float, kOnePassVecs[1]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
                                             loss, g_max, g_sumexp_m1, grad_expected, grad_assumed,
-                                            gout_div, st);
+                                            target_bad, gout_div, st);
   } else {
     if (small)
       launch_fwdbwd<uint16_t, kOnePassVecs[0]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
                                                loss, g_max, g_sumexp_m1, grad_expected,
-                                               grad_assumed, gout_div, st);
+                                               grad_assumed, target_bad, gout_div, st);
     else
       launch_fwdbwd<uint16_t, kOnePassVecs[1]>(logits, grad, n_rows, vocab, ld, ld_grad, target,
                                                loss, g_max, g_sumexp_m1, grad_expected,
-                                               grad_assumed, gout_div, st);
+                                               grad_assumed, target_bad, gout_div, st);
   }
   return launch_status();
 }

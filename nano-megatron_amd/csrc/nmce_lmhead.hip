@@ -691,32 +691,193 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   }
 }
 
+// The fp32 epilogues (modes 1-3 of gemm_store_kernel). The 256x256 fp32 tile
+// goes through the freed LDS in two passes of 128 rows: pass q takes
+// accumulators fm = 2q, 2q + 1 of every wave, i.e. tile rows 64 q .. 64 q + 63
+// and 128 + 64 q .. 128 + 64 q + 63, so each pass reads its own half of the
+// accumulator registers. Staged row r (1 KiB) is tile row
+// 128 (r >> 6) + 64 q + (r & 63); its 16-byte chunk c sits at c ^ 8 ((r >> 2)
+// & 1), which puts the two rows one ds_write_b32 covers (r and r + 4) on
+// opposite halves of the banks. Every thread then moves 16 chunks: staged row
+// 8 p + wave, chunk lane, so a wave's access is one 1 KiB row segment of Cf
+// (or 512 bytes of C).
+// kVec (N % 4 == 0, ldc % 4 == 0, Cf 16-byte and C 8-byte aligned, 512 rows
+// within 32-bit offsets): buffer resources on the wave's first row, the
+// lane's column in the one offset register and the row step in the scalar
+// offset. The hardware range check covers the per-lane offset only, so rows
+// past M (passes p >= np, uniform) are skipped explicitly, and a lane whose
+// columns lie past N gets the resource's size as its offset: its accesses
+// are out of range (no memory access, a load reads 0, a store is dropped)
+// whether or not the scalar offset takes part in the check. Every access
+// left is inside the matrix. In modes 2 and 3 half of the 16 loads of Cf
+// are issued before the pass is staged, so their latency runs under the
+// staging, and the other half right after it. Cf is streamed (non-temporal)
+// both ways. Without kVec the pass leaves element by element.
+//   kMode 1: Cf = acc;  kMode 2: Cf += acc;  kMode 3: C = bf16(Cf + acc)
+template <int kMode, bool kVec>
+__device__ __forceinline__ void store_f32_tile(const Acc& acc, char* lds, float* __restrict__ Cf,
+                                               uint16_t* __restrict__ C, int64_t ldc, int64_t M,
+                                               int64_t N, int64_t m0, int64_t n0) {
+  static_assert(kMode >= 1 && kMode <= 3, "fp32 epilogue modes");
+  static_assert(kBN == 256 && kWavesM == 2 && kFM == 4 && 128 * kBN * 4 <= kLdsBytes,
+                "two passes of 128 rows fit the stages");
+  constexpr int kRowsPerPass = kThreads / 64;  // 8
+  constexpr int kPasses = 128 / kRowsPerPass;  // 16
+  constexpr int kNt = 2;                       // cache policy: non-temporal
+  // Loads of Cf issued before a pass is staged (the staging needs registers
+  // for the accumulators it moves); the rest follow right after it.
+  constexpr int kEarly = 8;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int fhalf = lane >> 5;
+  float* S = reinterpret_cast<float*>(lds);
+  const bool col_ok = n0 + 4 * lane < N;
+  // Tile rows of staged rows 8 p + wave, relative to the pass's first row.
+  auto row_off = [](int p) { return 8 * p + 64 * (p >> 3); };
+  __syncthreads();  // every wave is done with the operand buffers
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int64_t row0 = m0 + 64 * q + wave;  // tile row of staged row `wave`
+    // valid passes: a prefix, rows increase with p
+    int np = 0;
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) np += (row0 + row_off(p) < M) ? 1 : 0;
+    np = __builtin_amdgcn_readfirstlane(np);
+    const int64_t lim = np == 0 ? 0 : (np < kPasses ? row_off(np) : row_off(kPasses - 1) + 1);
+    const uint32_t vf = col_ok ? static_cast<uint32_t>(lane) * 16u
+                               : static_cast<uint32_t>(lim * ldc * 4);
+    float* cf_base = Cf + (np > 0 ? row0 : 0) * ldc + n0;
+    u32x4 old[kPasses];
+    __amdgpu_buffer_rsrc_t rf;
+    if constexpr (kVec) {
+      rf = __builtin_amdgcn_make_buffer_rsrc(cf_base, 0, static_cast<int>(lim * ldc * 4),
+                                             0x00020000);
+      if constexpr (kMode >= 2) {
+#pragma unroll
+        for (int p = 0; p < kEarly; ++p) {
+          if (p < np)
+            old[p] = __builtin_amdgcn_raw_buffer_load_b128(
+                rf, vf, static_cast<uint32_t>(row_off(p) * ldc * 4), kNt);
+        }
+      }
+    }
+#pragma unroll
+    for (int fn = 0; fn < kFN; ++fn) {
+      const int c = wn * kWaveN + 32 * fn + (lane & 31);
+#pragma unroll
+      for (int f = 0; f < 2; ++f)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int r = wm * 64 + 32 * f + 8 * (e >> 2) + 4 * fhalf + (e & 3);
+          S[r * kBN + ((((c >> 2) ^ (fhalf << 3)) << 2) | (c & 3))] = acc.c[2 * q + f][fn][e];
+        }
+    }
+    __syncthreads();
+    if constexpr (kVec && kMode >= 2) {
+#pragma unroll
+      for (int p = kEarly; p < kPasses; ++p) {
+        if (p < np)
+          old[p] = __builtin_amdgcn_raw_buffer_load_b128(
+              rf, vf, static_cast<uint32_t>(row_off(p) * ldc * 4), kNt);
+      }
+    }
+    const int sw = ((wave >> 2) & 1) << 3;  // chunk swizzle of staged rows 8 p + wave
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      const int r = p * kRowsPerPass + wave;
+      const u32x4 sv = *reinterpret_cast<const u32x4*>(S + r * kBN + ((lane ^ sw) << 2));
+      if constexpr (!kVec) {
+        const int64_t row = row0 + row_off(p);
+        const float sf[4] = {__uint_as_float(sv.x), __uint_as_float(sv.y), __uint_as_float(sv.z),
+                             __uint_as_float(sv.w)};
+        for (int j = 0; j < 4; ++j) {
+          const int64_t col = n0 + 4 * lane + j;
+          if (row >= M || col >= N) continue;
+          const int64_t o = row * ldc + col;
+          if constexpr (kMode == 1) Cf[o] = sf[j];
+          if constexpr (kMode == 2) Cf[o] += sf[j];
+          if constexpr (kMode == 3) C[o] = f32_to_bf16(Cf[o] + sf[j]);
+        }
+      } else {
+        if (p >= np) continue;
+        const uint32_t so = static_cast<uint32_t>(row_off(p) * ldc * 4);
+        if constexpr (kMode == 1) {
+          __builtin_amdgcn_raw_buffer_store_b128(sv, rf, vf, so, kNt);
+        } else {
+          const u32x4 o = old[p];
+          const float v0 = __uint_as_float(sv.x) + __uint_as_float(o.x);
+          const float v1 = __uint_as_float(sv.y) + __uint_as_float(o.y);
+          const float v2 = __uint_as_float(sv.z) + __uint_as_float(o.z);
+          const float v3 = __uint_as_float(sv.w) + __uint_as_float(o.w);
+          if constexpr (kMode == 2) {
+            __builtin_amdgcn_raw_buffer_store_b128(
+                u32x4{__float_as_uint(v0), __float_as_uint(v1), __float_as_uint(v2),
+                      __float_as_uint(v3)},
+                rf, vf, so, kNt);
+          } else {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const auto rh = __builtin_amdgcn_make_buffer_rsrc(
+                C + (np > 0 ? row0 : 0) * ldc + n0, 0, static_cast<int>(lim * ldc * 2), 0x00020000);
+            __builtin_amdgcn_raw_buffer_store_b64(
+                u32x2{pack_bf16x2(v0, v1), pack_bf16x2(v2, v3)}, rh,
+                col_ok ? static_cast<uint32_t>(lane) * 8u : static_cast<uint32_t>(lim * ldc * 2),
+                static_cast<uint32_t>(row_off(p) * ldc * 2), 0);
+          }
+        }
+      }
+    }
+    __syncthreads();  // the next pass reuses S
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Plain GEMM with a stored result: C[m, n] (ldc) for m < M, n < N.
 //   kMode 0: C = acc as bf16
 //   kMode 1: Cf = acc (fp32)
 //   kMode 2: Cf += acc (fp32)
 //   kMode 3: C = bf16(Cf + acc)
+// Split K (splits > 1, mode 1 only): the grid holds `splits` copies of the
+// tile grid; copy s takes k in [s ks, min((s + 1) ks, K)) and writes its
+// partial product to Cf + s * split_stride. Copies are numbered as extra tile
+// rows (split-major), so the XCD bands keep tiles of one K range together.
+// kVec (modes 1-3): the output meets store_f32_tile's conditions for 16-byte
+// accesses (the host checks them); otherwise the half tiles leave element by
+// element.
 // ---------------------------------------------------------------------------
-template <int kMode, bool kAMN = false, bool kBMN = false>
+template <int kMode, bool kAMN = false, bool kBMN = false, bool kVec = true>
 __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
     const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
     int64_t ldb, int64_t N, int64_t K, uint16_t* __restrict__ C, float* __restrict__ Cf,
-    int64_t ldc, int group_m, int64_t ka_rows, int64_t kb_rows) {
+    int64_t ldc, int group_m, int64_t ka_rows, int64_t kb_rows, int splits, int64_t ks,
+    int64_t split_stride) {
   extern __shared__ __align__(16) char lds[];
   const int tiles_m = static_cast<int>((M + kBM - 1) / kBM);
   const int tiles_n = static_cast<int>((N + kBN - 1) / kBN);
-  int tm, tn;
-  tile_coords(group_m, tiles_m, tiles_n, tm, tn);
+  int tmv, tn;
+  tile_coords(group_m, tiles_m * splits, tiles_n, tmv, tn);
+  const int split = tmv / tiles_m;
+  const int tm = tmv - split * tiles_m;
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
+  // This copy's K range: the operands start at its first k (a k-column of a
+  // K-contiguous operand, a k-row of an MN-contiguous one).
+  const int64_t k0 = split * ks;
+  const int64_t kl = (K - k0) < ks ? (K - k0) : ks;
+  const uint16_t* As = kAMN ? A + k0 * lda : A + k0;
+  const uint16_t* Bs = kBMN ? B + k0 * ldb : B + k0;
+  Cf += split * split_stride;
   Acc acc;
-  gemm_mainloop<kAMN, kBMN>(A, lda, M, B, ldb, N, K, m0, n0, lds, acc, ka_rows, kb_rows);
+  gemm_mainloop<kAMN, kBMN>(As, lda, M, Bs, ldb, N, kl, m0, n0, lds, acc, ka_rows - k0,
+                            kb_rows - k0);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int wm = wave / kWavesN, wn = wave % kWavesN;
   const int fhalf = lane >> 5;
-  if constexpr (kMode == 0) {
+  if constexpr (kMode != 0) {
+    store_f32_tile<kMode, kVec>(acc, lds, Cf, C, ldc, M, N, m0, n0);
+    return;
+  } else {
     // bf16 out through the freed LDS, as lmhead_p_kernel stages P^T: words
     // of two rows (vp = row / 2) per column, columns XOR-swizzled by the row
     // pair, then 16-byte stores of 512-byte row segments. Tiles that reach
@@ -766,25 +927,6 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
         }
       }
     }
-    return;
-  }
-#pragma unroll
-  for (int fn = 0; fn < kFN; ++fn) {
-    const int64_t col = n0 + wn * kWaveN + 32 * fn + (lane & 31);
-    if (col >= N) continue;
-#pragma unroll
-    for (int fm = 0; fm < kFM; ++fm)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int64_t row = m0 + wm * kWaveM + acc_row(fm, e, fhalf);
-        if (row >= M) continue;
-        const int64_t o = row * ldc + col;
-        const float v = acc.c[fm][fn][e];
-        if constexpr (kMode == 0) C[o] = f32_to_bf16(v);
-        if constexpr (kMode == 1) Cf[o] = v;
-        if constexpr (kMode == 2) Cf[o] += v;
-        if constexpr (kMode == 3) C[o] = f32_to_bf16(Cf[o] + v);
-      }
   }
 }
 
@@ -1026,6 +1168,31 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
   }
 }
 
+// A product split over K (gemm_store_kernel, splits > 1) summed into bf16:
+// out[r * ldo + c] = bf16(sum_s part[s][r][c]) for r < M, c < N (N % 4 == 0),
+// with the partials [splits][M][N] fp32 contiguous. The splits are added in
+// order, so the result does not depend on how the GEMM was scheduled.
+__global__ __launch_bounds__(256) void split_sum_bf16_kernel(const float* __restrict__ part,
+                                                             int splits, int64_t M, int64_t N,
+                                                             uint16_t* __restrict__ out,
+                                                             int64_t ldo) {
+  const int64_t total = M * N;
+  const int64_t i = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) * 4;
+  if (i >= total) return;
+  float a[4];
+  Elem<float>::unpack(load_stream(reinterpret_cast<const u32x4*>(part + i)), a);
+  for (int sp = 1; sp < splits; ++sp) {
+    float b[4];
+    Elem<float>::unpack(load_stream(reinterpret_cast<const u32x4*>(part + sp * total + i)), b);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) a[k] += b[k];
+  }
+  const int64_t r = i / N, c = i - r * N;
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  *reinterpret_cast<u32x2*>(out + r * ldo + c) = u32x2{pack_bf16x2(a[0], a[1]),
+                                                       pack_bf16x2(a[2], a[3])};
+}
+
 // bf16 transpose with zero padding: out[c * ldo + r] = in[r * ldi + c] for
 // r < R, c < C; out[c * ldo + r] = 0 for R <= r < ldo. 64x64 tiles through
 // LDS; interior tiles move 16 bytes per load and per store (ldi, ldo and the
@@ -1097,15 +1264,6 @@ int configure_lds() {
       reinterpret_cast<const void*>(&lmhead_stats_kernel),
       reinterpret_cast<const void*>(&lmhead_dz_kernel),
       reinterpret_cast<const void*>(&lmhead_p_kernel),
-      reinterpret_cast<const void*>(&gemm_store_kernel<0>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<1>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<2>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<3>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<0, true, true>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<0, false, true>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<1, false, true>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<2, false, true>),
-      reinterpret_cast<const void*>(&gemm_store_kernel<3, false, true>),
   };
   for (const void* k : kernels) {
     const hipError_t e =
@@ -1124,27 +1282,57 @@ inline bool operand_ok(const void* p, int64_t ld) {
 
 // The product kernels by output mode and operand layout: K-contiguous A, and
 // B K-contiguous (b_mn = false) or MN-contiguous with kb_rows k-rows (b_mn;
-// then A may be MN-contiguous too, a_mn, in mode 0 only).
-template <int kMode, bool kAMN, bool kBMN>
-void launch_store(dim3 grid, hipStream_t stream, const uint16_t* A, int64_t lda, int64_t M,
-                  const uint16_t* B, int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf,
-                  int64_t ldc, int group_m, int64_t ka_rows, int64_t kb_rows) {
-  hipLaunchKernelGGL((gemm_store_kernel<kMode, kAMN, kBMN>), grid, dim3(kThreads), kLdsBytes,
-                     stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m, ka_rows, kb_rows);
+// then A may be MN-contiguous too, a_mn, in modes 0 and 1 only).
+template <int kMode, bool kAMN, bool kBMN, bool kVec>
+int launch_store(dim3 grid, hipStream_t stream, const uint16_t* A, int64_t lda, int64_t M,
+                 const uint16_t* B, int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf,
+                 int64_t ldc, int group_m, int64_t ka_rows, int64_t kb_rows, int splits,
+                 int64_t ks, int64_t split_stride) {
+  static bool lds_set = false;  // the attribute is set once per process and kernel
+  if (!lds_set) {
+    const hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&gemm_store_kernel<kMode, kAMN, kBMN, kVec>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
+    if (e != hipSuccess) return static_cast<int>(e);
+    lds_set = true;
+  }
+  hipLaunchKernelGGL((gemm_store_kernel<kMode, kAMN, kBMN, kVec>), grid, dim3(kThreads),
+                     kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m, ka_rows,
+                     kb_rows, splits, ks, split_stride);
+  return NMCE_OK;
 }
 
+// splits > 1 (mode 1 only): K in `splits` ranges of ks (a multiple of kBK;
+// the last one may be shorter), partial products at Cf + s * split_stride.
 int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const uint16_t* B,
                       int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf, int64_t ldc,
                       hipStream_t stream, int group_m = kGroupM, bool a_mn = false,
-                      bool b_mn = false, int64_t ka_rows = 0, int64_t kb_rows = 0) {
-  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN);
+                      bool b_mn = false, int64_t ka_rows = 0, int64_t kb_rows = 0,
+                      int splits = 1, int64_t ks = 0, int64_t split_stride = 0) {
+  if (splits < 1 || (splits > 1 && (mode != 1 || ks <= 0 || ks % kBK != 0 ||
+                                    (splits - 1) * ks >= K)))
+    return NMCE_EINVAL_SHAPE;
+  if (splits == 1) ks = K;
+  const int64_t tiles = ((M + kBM - 1) / kBM) * ((N + kBN - 1) / kBN) * splits;
   const dim3 grid(static_cast<unsigned>(tiles));
-  if (a_mn && (!b_mn || mode != 0)) return NMCE_EINVAL_SHAPE;
-#define NMCE_STORE(MODE, AMN, BMN)                                                        \
-  launch_store<MODE, AMN, BMN>(grid, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m, \
-                               ka_rows, kb_rows)
+  if (a_mn && (!b_mn || mode > 1)) return NMCE_EINVAL_SHAPE;
+  // The fp32 epilogues' 16-byte form: whole 16-byte chunks, aligned outputs,
+  // and every offset (a pass's 185 rows, plus as much again for a lane past
+  // N) within 32 bits.
+  const bool vec = (N & 3) == 0 && (ldc & 3) == 0 && (reinterpret_cast<uintptr_t>(Cf) & 15) == 0 &&
+                   (mode != 3 || (reinterpret_cast<uintptr_t>(C) & 7) == 0) &&
+                   ldc * 4 * 512 < (int64_t{1} << 32);
+  int st = NMCE_OK;
+#define NMCE_STORE(MODE, AMN, BMN)                                                           \
+  st = vec ? launch_store<MODE, AMN, BMN, true>(grid, stream, A, lda, M, B, ldb, N, K, C, Cf, \
+                                                ldc, group_m, ka_rows, kb_rows, splits, ks,   \
+                                                split_stride)                                 \
+           : launch_store<MODE, AMN, BMN, false>(grid, stream, A, lda, M, B, ldb, N, K, C, Cf, \
+                                                 ldc, group_m, ka_rows, kb_rows, splits, ks,  \
+                                                 split_stride)
   if (a_mn) {
-    NMCE_STORE(0, true, true);
+    if (mode == 0) NMCE_STORE(0, true, true);
+    else NMCE_STORE(1, true, true);
   } else if (b_mn) {
     switch (mode) {
       case 0: NMCE_STORE(0, false, true); break;
@@ -1161,6 +1349,7 @@ int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const
     }
   }
 #undef NMCE_STORE
+  if (st) return st;
   return launch_status();
 }
 
@@ -1203,6 +1392,51 @@ BwdLayout bwd_layout(int64_t n, int64_t h, int64_t v, int64_t chunk) {
 
 int64_t fwd_partial_blocks(int64_t v) { return (v + kPartialRows - 1) / kPartialRows; }
 
+// Compute units of the current device (256 if the query fails).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  int n_cu = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (cus[dev] == 0) {
+      int v = 0;
+      if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess &&
+          v > 0)
+        cus[dev] = v;
+    }
+    if (cus[dev] > 0) n_cu = cus[dev];
+  }
+  return n_cu;
+}
+
+// K ranges for a product of `tiles` output tiles over K (a multiple of kBK)
+// on `cus` compute units, one 256x256 tile per compute unit at a time: the
+// fewest ranges (at most 8, each at least 2048 long, each holding some of the
+// first `k_valid` k) whose rounds of tiles leave at most 5% of the compute
+// units idle, else the fewest with the least idle share. ks gets the range
+// length (a multiple of kBK).
+int choose_splits(int64_t tiles, int64_t K, int64_t k_valid, int cus, int64_t* ks) {
+  int best = 1;
+  double best_idle = 1e30;
+  for (int s = 1; s <= 8; ++s) {
+    const int64_t len = round_up((K + s - 1) / s, kBK);
+    if (s > 1 && (K / s < 2048 || (s - 1) * len >= K || (s - 1) * len >= k_valid)) break;
+    const int64_t t = tiles * s;
+    const int64_t rounds = (t + cus - 1) / cus;
+    const double idle = static_cast<double>(rounds * cus) / static_cast<double>(t);
+    if (idle <= 1.05) {
+      best = s;
+      break;
+    }
+    if (idle < best_idle - 1e-9) {
+      best_idle = idle;
+      best = s;
+    }
+  }
+  *ks = best == 1 ? K : round_up((K + best - 1) / best, kBK);
+  return best;
+}
+
 // Workspace of the one-pass fused loss (all offsets 256-byte aligned).
 struct FusedLayout {
   int64_t chunk;     // tokens per chunk (the last one may hold fewer)
@@ -1211,6 +1445,9 @@ struct FusedLayout {
   int64_t vpad;      // vocabulary padded to 256: rows of P^T, K of the dX GEMM
   int64_t nb;        // 128-row blocks of partial statistics
   int64_t off_pt, off_part, off_acc, total;
+  int64_t dx_splits;  // K ranges of a chunk's dX product (split K when its tiles are few)
+  int64_t dx_ks;      // their length
+  int64_t off_dxp;    // their fp32 partials [dx_splits][chunk][h] (dx_splits > 1)
 };
 
 FusedLayout fused_layout(int64_t n, int64_t h, int64_t v, int64_t token_chunk) {
@@ -1221,10 +1458,13 @@ FusedLayout fused_layout(int64_t n, int64_t h, int64_t v, int64_t token_chunk) {
   L.ldt = round_up(L.chunk, 64);
   L.vpad = round_up(v, kBM);
   L.nb = fwd_partial_blocks(v);
+  const int64_t dx_tiles = ((L.chunk + kBM - 1) / kBM) * ((h + kBN - 1) / kBN);
+  L.dx_splits = choose_splits(dx_tiles, L.vpad, v, device_cus(), &L.dx_ks);
   int64_t off = 0;
   L.off_pt = off; off += align256(L.vpad * L.ldt * 2);
   L.off_part = off; off += align256(3 * L.nb * L.chunk * 4);
   L.off_acc = off; off += L.n_chunks > 1 ? align256(v * h * 4) : 0;
+  L.off_dxp = off; off += L.dx_splits > 1 ? align256(L.dx_splits * L.chunk * h * 4) : 0;
   L.total = off;
   return L;
 }
@@ -1547,7 +1787,8 @@ int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t voc
   if (n_rows < 1 || hidden_size < 1 || vocab_local < 1) return NMCE_EINVAL_SHAPE;
   const FusedLayout L = fused_layout(n_rows, hidden_size, vocab_local, token_chunk);
   const int64_t v[NMCE_LMHEAD_FUSED_LAYOUT_FIELDS] = {
-      L.total, L.chunk, L.n_chunks, L.ldt, L.vpad, L.nb, L.off_pt, L.off_part, L.off_acc};
+      L.total,  L.chunk,    L.n_chunks, L.ldt,    L.vpad,     L.nb,
+      L.off_pt, L.off_part, L.off_acc,  L.off_dxp, L.dx_splits};
   for (int i = 0; i < NMCE_LMHEAD_FUSED_LAYOUT_FIELDS; ++i) layout[i] = v[i];
   return NMCE_OK;
 }
@@ -1631,11 +1872,24 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
   if ((st = launch_status())) return st;
   // dX rows of the chunk = dZ_c W: both operands read as they lie, k-row
   // (vocabulary) major: dZ^T [vpad, ldt] and W [V, H] (K = the padded
-  // vocabulary; dZ^T is zero past V, so W's k-rows stop at V).
-  if ((st = launch_gemm_store(0, pt, L.ldt, nc, W, H, H, L.vpad,
-                              static_cast<uint16_t*>(grad_hidden) + t0 * H, nullptr, H, s,
-                              kGroupMProducts, true, true, L.vpad, V)))
-    return st;
+  // vocabulary; dZ^T is zero past V, so W's k-rows stop at V). A chunk with
+  // too few tiles to fill the device splits K and sums the fp32 partials.
+  uint16_t* dx_rows = static_cast<uint16_t*>(grad_hidden) + t0 * H;
+  if (L.dx_splits == 1) {
+    if ((st = launch_gemm_store(0, pt, L.ldt, nc, W, H, H, L.vpad, dx_rows, nullptr, H, s,
+                                kGroupMProducts, true, true, L.vpad, V)))
+      return st;
+  } else {
+    float* part = reinterpret_cast<float*>(ws + L.off_dxp);
+    if ((st = launch_gemm_store(1, pt, L.ldt, nc, W, H, H, L.vpad, nullptr, part, H, s,
+                                kGroupMProducts, true, true, L.vpad, V,
+                                static_cast<int>(L.dx_splits), L.dx_ks, nc * H)))
+      return st;
+    const int64_t quads = nc * H / 4;
+    hipLaunchKernelGGL(split_sum_bf16_kernel, dim3(static_cast<unsigned>((quads + 255) / 256)),
+                       dim3(256), 0, s, part, static_cast<int>(L.dx_splits), nc, H, dx_rows, H);
+    if ((st = launch_status())) return st;
+  }
   // dW (+)= dZ_c^T X_c: A = dZ^T (K = the chunk's padded tokens contiguous),
   // B = the chunk's rows of X as they lie, token-major (zero dZ^T columns past
   // the chunk, so X's k-rows stop at nc). Accumulated in fp32 across chunks

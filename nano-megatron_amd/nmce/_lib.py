@@ -35,6 +35,7 @@ SIGNATURES: dict[str, tuple] = {
     "nmce_ce_combine": (_c_int, [_p, _p, _p, _c_int, _i64, _i64, _p, _p, _p, _p]),
     "nmce_validate_slots": (_i64, [_i64]),
     "nmce_validate_targets": (_c_int, [_p, _i64, _i64, _p, _p]),
+    "nmce_validate_targets_once": (_c_int, [_p, _i64, _i64, _p, _p, _p]),
     "nmce_stream_copy": (_c_int, [_p, _p, _i64, _p]),
     "nmce_ce_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64, _p]),
     "nmce_ce_bwd_scaled": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _i64, _p, _p, _p, _i64,
@@ -43,7 +44,7 @@ SIGNATURES: dict[str, tuple] = {
                                            _p, _p, ctypes.c_float, _p, _p, _p]),
     "nmce_ce_fwd_bwd_max_vocab": (_i64, [_c_int]),
     "nmce_ce_fwd_bwd": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p,
-                                 ctypes.c_float, _p]),
+                                 _p, ctypes.c_float, _p]),
     "nmce_ce_grad_rescale_unless": (_c_int, [_p, _c_int, _i64, _i64, _i64, _p, _p, _p, _p]),
     "nmce_lmhead_ce_fwd_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "nmce_lmhead_ce_fwd_stats": (_c_int, [_p, _p, _c_int, _i64, _i64, _i64, _p, _i64, _p, _p, _p,
@@ -69,7 +70,7 @@ SIGNATURES: dict[str, tuple] = {
 }
 
 NMCE_LMHEAD_LAYOUT_FIELDS = 10
-NMCE_LMHEAD_FUSED_LAYOUT_FIELDS = 9
+NMCE_LMHEAD_FUSED_LAYOUT_FIELDS = 11
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

@@ -25,21 +25,26 @@ Differences from the reference, all deliberate:
   ``loss.backward()``, before the first) -- as the reference's forward
   computes the softmax its backward returns (:48-49). A loss scaled the same
   way every step keeps the forward's gradient from the second step on. The
-  gradient goes into the logits' storage when the gradient is written in
-  place (below), else into a new ``[tokens, vocab]`` buffer. A backward whose
-  upstream value differs rewrites a separate buffer from the logits
-  (bit-identical to the two-pass path), and rescales an in-place one (within
-  four fp32 or two bf16 units in the last place: the written gradient and the
-  ratio are each rounded once; exact for a power-of-two ratio).
-  ``one_pass=False`` turns it off.
-* The gradient is written **in place** into the logits storage when the
-  logits are a non-leaf tensor (as at model.py:277-281, where they come
-  straight from the LM-head matmul, which does not save them): by the
-  backward on the two-pass path, and already by the forward on the one-pass
-  path. Pass ``inplace=False`` to keep the logits intact; leaf tensors are
-  never overwritten. The version counter of the logits is bumped after an
+  gradient goes into a new ``[tokens, vocab]`` buffer, or into the logits'
+  own storage when the caller asks for that with ``inplace=True``. A
+  backward whose upstream value differs rewrites a separate buffer from the
+  logits (bit-identical to the two-pass path), and rescales an in-place one
+  (within four fp32 or two bf16 units in the last place: the written
+  gradient and the ratio are each rounded once; exact for a power-of-two
+  ratio). ``one_pass=False`` turns it off.
+* The gradient is written **in place** into the logits storage with
+  ``inplace=True`` (as at model.py:277-281, where the logits come straight
+  from the LM-head matmul, which does not save them): by the forward on the
+  one-pass path, by the backward on the two-pass path. With the default
+  ``inplace=None`` the forward never writes into the logits: the one-pass
+  path writes a new buffer, and the two-pass backward writes into non-leaf
+  logits only once the backward runs (the forward has returned by then).
+  ``inplace=False`` never writes into them; leaf tensors are never
+  overwritten. The version counter of the logits is bumped after an
   in-place write, so any other autograd node that saved them fails loudly
-  instead of reading gradients.
+  instead of reading gradients. A target outside the vocabulary leaves the
+  logits untouched on every path: the one-pass kernel reads a flag that the
+  target check sets on the same stream before it writes anything.
 * With ``tp_size > 1`` the three dependent all-reduces (:23, :38, :43) become
   one all-gather of packed ``[3, tokens]`` statistics followed by a local
   combine.
@@ -217,7 +222,8 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
 
 
 def launch_target_check(target: torch.Tensor, vocab_size: int,
-                        on_side_stream: bool = True) -> _PendingCheck | None:
+                        on_side_stream: bool = True,
+                        device_flag: torch.Tensor | None = None) -> _PendingCheck | None:
     """Start the target check of cross_entropy.py:79-81 without blocking.
 
     One kernel counts targets outside ``[0, vocab_size)`` straight into pinned
@@ -225,6 +231,10 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
     current stream; ``raise_if_bad()`` on the result waits for that kernel
     alone. The loss kernels go on the current stream meanwhile, so the check
     adds nothing to the loss stream's timeline.
+
+    With ``device_flag`` (a one-element int32 device tensor) the check runs on
+    the current stream as one workgroup that also writes the count there, for
+    a loss kernel enqueued next that must write nothing on a bad target.
     """
     lib = _lib.load()
     t = target.reshape(-1)
@@ -233,9 +243,18 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
     n = t.numel()
     if n == 0:
         return None
-    slots = lib.nmce_validate_slots(n)
+    slots = 1 if device_flag is not None else lib.nmce_validate_slots(n)
     dev_index = t.device.index if t.device.index is not None else torch.cuda.current_device()
     host, event = _check_slot(dev_index, slots)
+    if device_flag is not None:
+        _launch("nmce_validate_targets", lib.nmce_validate_targets_once, t.data_ptr(), n,
+                vocab_size, host.data_ptr(), device_flag.data_ptr(),
+                _lib.stream_handle(t.device))
+        if dev_index == torch.cuda.current_device():
+            event.record()
+        else:
+            event.record(torch.cuda.current_stream(t.device))
+        return _PendingCheck(dev_index, host, event, slots)
     if not on_side_stream:
         # On the loss stream, ahead of a kernel that fills every compute unit
         # for its whole run (the one-pass forward), so that the host's wait
@@ -289,11 +308,15 @@ def _exchange_stats(local: torch.Tensor, group, world_size: int) -> torch.Tensor
     return gathered.to(local.device) if host else gathered
 
 
-def _resolve_inplace(logits: torch.Tensor, inplace) -> bool:
-    """``inplace=None``: in place iff the logits are a non-leaf tensor. A leaf
-    that requires grad is never overwritten."""
+def _resolve_inplace(logits: torch.Tensor, inplace, in_forward: bool = False) -> bool:
+    """Whether the gradient goes into the logits' storage. ``inplace=None``:
+    for a gradient written by the backward (two-pass path), in place iff the
+    logits are a non-leaf tensor; for one written by the forward (one-pass
+    path), never, so the logits read the same after the call returns.
+    ``inplace=True`` asks for it either way; a leaf that requires grad is
+    never overwritten."""
     if inplace is None:
-        return logits.grad_fn is not None
+        return (not in_forward) and logits.grad_fn is not None
     if inplace and logits.grad_fn is None and logits.requires_grad:
         raise ValueError("nmce: refusing to write the gradient into a leaf tensor; "
                          "pass inplace=False or None")
@@ -375,12 +398,15 @@ def _one_pass_rows(logits: torch.Tensor, world_size: int) -> torch.Tensor | None
 _one_pass_limit: dict[int, int] = {}
 
 
-def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint, inplace):
+def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint, inplace,
+                         bad_flag=None):
     """Forward of the whole vocabulary that also writes the gradient of the mean
     for the upstream value in ``hint`` (nmce_ce_fwd_bwd), from the same single
     read of the logits: into the logits' own storage when ``inplace``, else
     into a new buffer. Returns the flat per-token loss; the backward keeps that
-    gradient unless its upstream value differs."""
+    gradient unless its upstream value differs. ``bad_flag``: the device count
+    of the target check enqueued just before; the kernel writes nothing when
+    it is nonzero."""
     _check_inputs(logits, target, vocab_start, vocab_end)
     lib = _lib.load()
     dev = logits.device
@@ -399,7 +425,7 @@ def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint
     _launch("nmce_ce_fwd_bwd", lib.nmce_ce_fwd_bwd, rows.data_ptr(), grad.data_ptr(),
             _lib.dtype_code(rows.dtype), n, V, ld, ldg, tgt.data_ptr(), loss.data_ptr(),
             row_stat[0].data_ptr(), row_stat[1].data_ptr(), hint.data_ptr(),
-            assumed.data_ptr(), float(n), _lib.stream_handle(dev))
+            assumed.data_ptr(), _lib.ptr(bad_flag), float(n), _lib.stream_handle(dev))
     ctx.vocab_start = vocab_start
     ctx.logits_shape = logits.shape
     ctx.ld = ld
@@ -531,14 +557,15 @@ class _VocabParallelCrossEntropyMean(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None,
-                hint=None):
+                hint=None, bad_flag=None):
         # ``hint`` (the one-pass path's upstream value) is given only when a
         # gradient is wanted; without it the forward writes no gradient.
         rows = _one_pass_rows(logits, world_size) if hint is not None else None
         ctx.one_pass = rows is not None
         if ctx.one_pass:
             loss = _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint,
-                                        _resolve_inplace(logits, inplace))
+                                        _resolve_inplace(logits, inplace, in_forward=True),
+                                        bad_flag)
         else:
             loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
                                inplace)
@@ -555,7 +582,7 @@ class _VocabParallelCrossEntropyMean(torch.autograd.Function):
             grad = _ce_backward_one_pass(ctx, go, gdiv)
         else:
             grad = _ce_backward(ctx, go, 0, gdiv)
-        return grad, None, None, None, None, None, None, None
+        return grad, None, None, None, None, None, None, None, None
 
 
 def vocab_parallel_cross_entropy(
@@ -577,25 +604,29 @@ def vocab_parallel_cross_entropy(
     0-dim fp32 tensor. ``validate=False`` skips the host-synchronising target
     check (the kernels never read out of bounds either way).
 
-    ``inplace=None`` writes the gradient into the logits' storage when they are
-    a non-leaf tensor (as the LM head's output is); ``False`` never does.
+    ``inplace=True`` writes the gradient into the logits' storage (the call
+    site at model.py:277-281 can: the LM head's output is read by nothing
+    else); ``None`` (default) does so only from the two-pass backward, for
+    non-leaf logits; ``False`` never does.
 
     At TP = 1, when a gradient is wanted (grad mode on, logits requiring grad)
     and the rows fit the one-pass kernel (V a whole number of 16-byte vectors,
     at most 131072 bf16 or 65536 fp32 columns, rows 16-byte aligned), the
     forward reads the logits once and also writes their gradient, for the
     upstream value the previous backward of this call site received (1.0 at
-    first): in place (the logits hold the gradient once the forward returns)
-    or into a new buffer. The backward redoes it only when its upstream value
-    differs: bit-identical to the two-pass path, which ``one_pass=False``
-    selects, for a new buffer; rescaled, within four fp32 or two bf16 units in
-    the last place, in place. ``upstream_hint`` (a one-element fp32 device tensor) replaces
-    the call site's value: the forward assumes what it holds and the backward
-    stores what it receives there.
+    first): in place with ``inplace=True`` (the logits hold the gradient once
+    the forward returns), else into a new buffer. The backward redoes it only
+    when its upstream value differs: bit-identical to the two-pass path, which
+    ``one_pass=False`` selects, for a new buffer; rescaled, within four fp32
+    or two bf16 units in the last place, in place. ``upstream_hint`` (a
+    one-element fp32 device tensor) replaces the call site's value: the
+    forward assumes what it holds and the backward stores what it receives
+    there.
 
-    On a target outside the vocabulary the ``ValueError`` is raised after the
-    loss kernels were enqueued; on the in-place one-pass path the logits then
-    already hold a (meaningless) gradient.
+    A target outside the vocabulary raises the reference's ``ValueError``
+    before this returns, and the logits are left as they were: on the
+    one-pass path the check runs on the loss stream and the kernel writes
+    nothing when it failed; the two-pass path writes only in its backward.
     """
     _check_inputs(logits, target, vocab_start, vocab_end)
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
@@ -608,14 +639,20 @@ def vocab_parallel_cross_entropy(
         else:
             _check_hint(upstream_hint, logits.device)
             hint = upstream_hint
-    pending = (launch_target_check(target, vocab_size, on_side_stream=hint is None)
+    bad_flag = None
+    if validate and hint is not None:
+        # the one-pass kernel reads the check's count before writing anything
+        bad_flag = torch.empty(1, dtype=torch.int32, device=logits.device)
+    pending = (launch_target_check(target, vocab_size, on_side_stream=hint is None,
+                                   device_flag=bad_flag)
                if validate else None)
     # The loss kernels are enqueued before the host waits for the check, so
     # the GPU is busy while the host reads the counts. They never read out of
     # bounds on a bad target; their result is discarded when the check fails.
     try:
         loss = _VocabParallelCrossEntropyMean.apply(
-            logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, hint)
+            logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, hint,
+            bad_flag)
     except BaseException:
         if pending is not None:
             pending.wait()

@@ -12,7 +12,10 @@ becomes
 with ``x`` the (already TP-mapped, model.py:188-191) hidden state and ``W`` the
 LM head's vocabulary shard ``[V/tp, H]``. The loss and its gradients with
 respect to ``x`` and ``W`` are those of the two-step reference, but the
-``[tokens, V/tp]`` logits are never stored.
+``[tokens, V/tp]`` logits are never stored: the one-pass path holds the
+bf16 exponentials of one chunk of tokens at a time (by default at most a
+quarter of them and at most 2 GiB), the recomputing path two bf16 copies of
+one vocabulary chunk's logit gradient.
 
 When a gradient is wanted (grad mode on, ``x`` or ``W`` requiring grad) the
 wrapper takes the one-pass path: the forward goes through the tokens in
@@ -54,38 +57,34 @@ from .mappings import (
 )
 from .parallel import divide
 
-# Default vocabulary rows per backward chunk: the chunk's logit gradient is
-# held twice in bf16 (4 * tokens * chunk bytes), so no tensor the size of the
-# full logits ever exists. A caller with memory to spare may pass a chunk that
-# covers the whole shard: the backward is then one dZ launch and one library
-# GEMM per product with no fp32 accumulation of dX (about 2% faster at
-# [16384, 4096] x [128256, 4096]), at the price of a full-size dZ.
+# Default vocabulary rows per chunk of the recomputing backward: the chunk's
+# logit gradient is held twice in bf16 (4 * tokens * chunk bytes), so no
+# tensor the size of the full logits ever exists. A chunk covering the whole
+# shard needs no fp32 accumulation of dX, at the price of a full-size dZ.
 DEFAULT_VOCAB_CHUNK = 32768
 
-# Who computes the two plain products of the backward (dW = dZ^T X and
-# dX += dZ W, on the K-contiguous X^T / W^T / dZ^T buffers the library
-# prepares): "library" uses torch.mm / torch.addmm (hipBLASLt, fp32
-# accumulation of dX across chunks), "nmce" the library's own MFMA GEMM
-# (nmce_lmhead_ce_bwd, everything in one C call). The fused parts -- the
-# forward statistics GEMM and the recomputation of dZ -- are libnmce kernels
-# either way.
-BACKWARD_GEMM = "nmce"
-
-# Bytes the one-pass path may hold for one chunk of tokens: the chunk's
-# exponentials, turned into its dZ^T in place, 2 * chunk * V bytes (bf16). The
-# default chunk is the most tokens (a multiple of 256) within this budget, all
-# of them when they fit: a 16384-token micro-batch at V = 256000 takes 7.8 GiB
-# of a 288 GB device, a quarter of the reference's fp32 logits and softmax for
-# the same tokens. One chunk needs no fp32 accumulation of dW across chunks,
-# which cost 3% of the step at [16384, 4096] x [128256, 4096] and 10% at
-# [16384, 3072] x [256000, 3072] (two chunks of 8192 against one of 16384).
-CHUNK_BUDGET_BYTES = 16 << 30
+# The one-pass path goes through the tokens in chunks. A chunk's
+# exponentials, turned into its dZ^T in place, take 2 * V * chunk bytes
+# (bf16), so the chunk bounds what the fused loss holds of the logits: by
+# default at most a quarter of the tokens (rounded up to whole 256-token
+# tiles; every token only when there are at most 256) and at most
+# CHUNK_BUDGET_BYTES, so nothing the size of the [tokens, V] logits is
+# allocated. dW is then accumulated in fp32 across the chunks, which the
+# accumulating GEMM epilogue does at little cost (measured on one MI355X:
+# [16384, 4096] x [128256, 4096] runs as fast in four chunks of 4096 tokens as
+# in one chunk; [16384, 3072] x [256000, 3072] 3% slower).
+CHUNK_BUDGET_BYTES = 2 << 30
+CHUNK_FRACTION = 4
 
 
 def default_token_chunk(n_tokens: int, vocab_local: int) -> int:
-    """Tokens per one-pass chunk within ``CHUNK_BUDGET_BYTES``."""
-    fit = CHUNK_BUDGET_BYTES // (2 * max(1, vocab_local)) // 256 * 256
-    return n_tokens if fit >= n_tokens else max(256, fit)
+    """Tokens per one-pass chunk: a quarter of the tokens rounded up to a
+    multiple of 256 (at least 256), and no more than fit
+    ``CHUNK_BUDGET_BYTES`` of bf16 exponentials (at least 256)."""
+    quarter = -(-n_tokens // CHUNK_FRACTION)
+    chunk = max(256, -(-quarter // 256) * 256)
+    fit = max(256, CHUNK_BUDGET_BYTES // (2 * max(1, vocab_local)) // 256 * 256)
+    return min(chunk, fit, max(n_tokens, 1))
 
 _ALIGN = 64  # hidden size granularity of the GEMM kernels
 
@@ -104,80 +103,13 @@ def _workspace(nbytes: int, device: torch.device) -> torch.Tensor:
     return torch.empty(max(int(nbytes), 16), dtype=torch.uint8, device=device)
 
 
-def _bwd_layout(lib, n: int, hp: int, v: int, chunk: int) -> dict:
-    import ctypes
-    buf = (ctypes.c_int64 * _lib.NMCE_LMHEAD_LAYOUT_FIELDS)()
-    _lib.check(lib.nmce_lmhead_ce_bwd_layout(n, hp, v, chunk, ctypes.addressof(buf)),
-               "nmce_lmhead_ce_bwd_layout")
-    keys = ("total", "ldt", "vpad", "chunk", "n_chunks", "off_xt", "off_wt", "off_dzt",
-            "off_dz", "off_acc")
-    return dict(zip(keys, (int(b) for b in buf)))
-
-
-def _bf16_view(ws: torch.Tensor, offset: int, rows: int, cols: int) -> torch.Tensor:
-    """A [rows, cols] bf16 view of the uint8 workspace at byte ``offset``."""
-    return ws[offset:offset + rows * cols * 2].view(torch.bfloat16).view(rows, cols)
-
-
-def _backward_library_gemm(lib, x, w, tgt, vocab_start, row_stat, go, gstride, vocab_chunk,
-                           dw):
-    """Chunked backward: libnmce recomputes dZ per vocabulary chunk; the two
-    plain products run as library GEMMs on the K-contiguous buffers (X^T, W^T,
-    dZ^T), accumulating dX in fp32 across chunks. Returns dX (bf16)."""
-    n, hp = x.shape
-    V = w.shape[0]
-    dev = x.device
-    stream = _lib.stream_handle(dev)
-    L = _bwd_layout(lib, n, hp, V, vocab_chunk)
-    ws = _workspace(L["total"], dev)
-    _launch("nmce_lmhead_ce_bwd_prepare", lib.nmce_lmhead_ce_bwd_prepare, x.data_ptr(),
-            w.data_ptr(), _lib.NMCE_BF16, n, hp, V, vocab_chunk, ws.data_ptr(), ws.numel(),
-            stream)
-    ldt, vpad, chunk = L["ldt"], L["vpad"], L["chunk"]
-    xt = _bf16_view(ws, L["off_xt"], hp, ldt)
-    wt = _bf16_view(ws, L["off_wt"], hp, vpad)
-    dzt = _bf16_view(ws, L["off_dzt"], chunk, ldt)
-    dz = _bf16_view(ws, L["off_dz"], n, chunk)
-    n_chunks = L["n_chunks"]
-    if n_chunks == 1:
-        # One chunk holds the whole shard: both products are single GEMMs and
-        # dX needs no fp32 accumulation buffer (the GEMM accumulates in fp32
-        # and rounds once).
-        _launch("nmce_lmhead_ce_bwd_dz", lib.nmce_lmhead_ce_bwd_dz, x.data_ptr(), w.data_ptr(),
-                _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), vocab_start, row_stat[0].data_ptr(),
-                row_stat[1].data_ptr(), go.data_ptr(), gstride, vocab_chunk, 0, ws.data_ptr(),
-                ws.numel(), stream)
-        mpad = (V + 255) // 256 * 256
-        torch.mm(dzt[:V], xt.t(), out=dw)
-        return torch.mm(dz[:, :mpad], wt[:, :mpad].t())
-    acc = torch.empty((n, hp), dtype=torch.float32, device=dev)
-    for c in range(n_chunks):
-        v0 = c * chunk
-        mvalid = min(chunk, V - v0)
-        mpad = (mvalid + 255) // 256 * 256
-        _launch("nmce_lmhead_ce_bwd_dz", lib.nmce_lmhead_ce_bwd_dz, x.data_ptr(), w.data_ptr(),
-                _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), vocab_start, row_stat[0].data_ptr(),
-                row_stat[1].data_ptr(), go.data_ptr(), gstride, vocab_chunk, c, ws.data_ptr(),
-                ws.numel(), stream)
-        # dW rows of this chunk: dZ^T_c [mvalid, ldt] x (X^T [hp, ldt])^T; the
-        # token padding of both operands is zero.
-        torch.mm(dzt[:mvalid], xt.t(), out=dw[v0:v0 + mvalid])
-        # dX (+)= dZ_c [n, mpad] x (W^T[:, v0:v0+mpad])^T; the vocabulary
-        # padding of both operands is zero.
-        wt_c = wt[:, v0:v0 + mpad].t()
-        if c == 0:
-            torch.mm(dz[:, :mpad], wt_c, out_dtype=torch.float32, out=acc)
-        else:
-            torch.addmm(acc, dz[:, :mpad], wt_c, out_dtype=torch.float32, out=acc)
-    return acc.to(torch.bfloat16)
-
-
 def _fused_layout(lib, n: int, hp: int, v: int, token_chunk: int) -> dict:
     import ctypes
     buf = (ctypes.c_int64 * _lib.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
     _lib.check(lib.nmce_lmhead_ce_fused_layout(n, hp, v, token_chunk, ctypes.addressof(buf)),
                "nmce_lmhead_ce_fused_layout")
-    keys = ("total", "chunk", "n_chunks", "ldt", "vpad", "nb", "off_pt", "off_part", "off_acc")
+    keys = ("total", "chunk", "n_chunks", "ldt", "vpad", "nb", "off_pt", "off_part", "off_acc",
+            "off_dxp", "dx_splits")
     return dict(zip(keys, (int(b) for b in buf)))
 
 
@@ -310,21 +242,19 @@ class _LMHeadVocabParallelCrossEntropyMean(torch.autograd.Function):
 
 def _recompute_backward(lib, x, w, tgt, vocab_start, row_stat, go, gstride, vocab_chunk, dw):
     """dX (returned) and dW (into ``dw``) by recomputing the logits one
-    vocabulary chunk at a time, on the route BACKWARD_GEMM names."""
+    vocabulary chunk at a time (nmce_lmhead_ce_bwd: the dZ kernel and the
+    library's own MFMA GEMM for both products)."""
     n, hp = x.shape
     V = w.shape[0]
     dev = x.device
-    if BACKWARD_GEMM == "nmce":
-        dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
-        ws = _workspace(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, hp, V, vocab_chunk), dev)
-        _launch("nmce_lmhead_ce_bwd", lib.nmce_lmhead_ce_bwd, x.data_ptr(), w.data_ptr(),
-                _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), vocab_start,
-                row_stat[0].data_ptr(), row_stat[1].data_ptr(), go.data_ptr(), gstride,
-                dx.data_ptr(), dw.data_ptr(), vocab_chunk, ws.data_ptr(), ws.numel(),
-                _lib.stream_handle(dev))
-        return dx
-    return _backward_library_gemm(lib, x, w, tgt, vocab_start, row_stat, go, gstride,
-                                  vocab_chunk, dw)
+    dx = torch.empty((n, hp), dtype=torch.bfloat16, device=dev)
+    ws = _workspace(lib.nmce_lmhead_ce_bwd_workspace_bytes(n, hp, V, vocab_chunk), dev)
+    _launch("nmce_lmhead_ce_bwd", lib.nmce_lmhead_ce_bwd, x.data_ptr(), w.data_ptr(),
+            _lib.NMCE_BF16, n, hp, V, tgt.data_ptr(), vocab_start,
+            row_stat[0].data_ptr(), row_stat[1].data_ptr(), go.data_ptr(), gstride,
+            dx.data_ptr(), dw.data_ptr(), vocab_chunk, ws.data_ptr(), ws.numel(),
+            _lib.stream_handle(dev))
+    return dx
 
 
 class _LMHeadVocabParallelCrossEntropy(torch.autograd.Function):
@@ -441,7 +371,9 @@ def lmhead_vocab_parallel_cross_entropy(
 
     When a gradient is wanted the forward is one pass (module docstring),
     going through ``token_chunk`` tokens at a time (default
-    ``default_token_chunk``: every token, within ``CHUNK_BUDGET_BYTES``) and assuming the upstream value held by
+    ``default_token_chunk``: a quarter of the tokens, within
+    ``CHUNK_BUDGET_BYTES``; pass the token count to hold every token's
+    exponentials at once) and assuming the upstream value held by
     ``upstream_hint`` (a one-element fp32 device tensor; default: one per
     call site). ``one_pass=False`` selects the forward that keeps only the
     row statistics, with a backward that recomputes the logits in chunks of

@@ -9,10 +9,11 @@ no CPU fallback.
 Modules
 -------
 ``ce_oracle``   numpy fp64 closed form, per-shard statistics, cross-shard
-                combine and gradient (follows nano_megatron/cross_entropy.py).
+                combine and gradient (follows nano_megatron/cross_entropy.py),
+                and the LM-head projection followed by the loss
+                (``lmhead_closed_form``, ``lmhead_sharded``; model.py:192).
 ``ce_restate``  torch-CPU restatement of the reference's op sequence in fp32,
                 used as the timed CPU baseline (``kind: "port"``).
-``lmhead_oracle`` fp32/fp64 LM-head projection + CE on token subsets.
 
 Pinning (what checks each function against something other than itself):
 see the module headers; each function lists its checks.

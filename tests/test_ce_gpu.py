@@ -877,8 +877,8 @@ def test_one_pass_hints_are_per_call_site(monkeypatch):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("shape", [(3, 37, 1000), (2, 512, 32000), (1, 600, 50304), (4, 8, 8)])
 def test_one_pass_in_place(dtype, shape):
-    """Non-leaf logits at TP = 1 (inplace=None): the one-pass forward writes the
-    gradient into the logits' own storage. Upstream 1.0 (the forward's value)
+    """Non-leaf logits at TP = 1 with inplace=True: the one-pass forward writes
+    the gradient into the logits' own storage. Upstream 1.0 (the forward's value)
     and 0.5 (a power-of-two rescale) are bit-identical to the two-pass path
     (which writes in place too, in its backward); 0.37 and 3.0 are rescaled
     and within four fp32 / two bf16 units in the last place (the written
@@ -902,7 +902,7 @@ def test_one_pass_in_place(dtype, shape):
             logits = base.clone() + anchor.to(dtype)  # non-leaf, own storage
             storage = logits.data_ptr()
             loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, one_pass=one_pass,
-                                                     upstream_hint=hint)
+                                                     upstream_hint=hint, inplace=True)
             grads = []
             logits.register_hook(lambda gr: grads.append(gr))
             (loss * upstream).backward()
@@ -974,10 +974,84 @@ def test_one_pass_retain_graph():
     assert torch.equal(grads[0][0].view(torch.int16), grads[1][0].view(torch.int16))
     assert torch.equal(grads[0][1].view(torch.int16), grads[1][1].view(torch.int16))
     anchor = torch.zeros((), device=DEV, requires_grad=True)
-    loss = nmce.vocab_parallel_cross_entropy(x.clone() + anchor.to(torch.bfloat16), t, 0, v, ctx)
+    loss = nmce.vocab_parallel_cross_entropy(x.clone() + anchor.to(torch.bfloat16), t, 0, v, ctx,
+                                             inplace=True)
     loss.backward(retain_graph=True)
     with pytest.raises(RuntimeError, match="second backward"):
         loss.backward()
+
+
+def test_one_pass_default_leaves_logits_readable():
+    """With the default inplace=None the one-pass forward writes its gradient
+    into a separate buffer: non-leaf logits read the same after the forward
+    (an accuracy metric or a log line computed from them is not corrupted)
+    and after the backward, and the gradient equals the in-place one."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(18)
+    n, v = 512, 50304
+    x = torch.randn(n, v, device=DEV, generator=g).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    grads = []
+    for inplace in (None, True):
+        hint = torch.ones(1, dtype=torch.float32, device=DEV)
+        anchor = torch.zeros((), device=DEV, requires_grad=True)
+        logits = x.clone() + anchor.to(torch.bfloat16)  # non-leaf, own storage
+        got = []
+        logits.register_hook(lambda gr: got.append(gr))
+        loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, inplace=inplace,
+                                                 upstream_hint=hint)
+        torch.cuda.synchronize()
+        if inplace is None:
+            assert torch.equal(logits.detach().view(torch.int16), x.view(torch.int16))
+            assert torch.equal(logits.detach().argmax(-1), x.argmax(-1))
+        loss.backward()
+        if inplace is None:
+            assert torch.equal(logits.detach().view(torch.int16), x.view(torch.int16))
+            assert got[0].data_ptr() != logits.data_ptr()
+        else:
+            assert got[0].data_ptr() == logits.data_ptr()
+        grads.append(got[0].detach().clone())
+    assert torch.equal(grads[0].view(torch.int16), grads[1].view(torch.int16))
+
+
+@pytest.mark.parametrize("v", [50304, 128256])
+def test_bad_target_leaves_in_place_logits_intact(v):
+    """A target outside the vocabulary on the in-place one-pass path (the
+    regular and the wide-row kernel): the wrapper raises the reference's
+    ValueError and the logits are bit for bit what they were (the kernel reads
+    the check's device flag and writes nothing), as the reference raises before
+    touching anything (cross_entropy.py:79-81). The next call with good targets
+    works as usual."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(19)
+    n = 300
+    x = torch.randn(n, v, device=DEV, generator=g).to(torch.bfloat16)
+    for bad in (v, -1, 10 ** 12):
+        print(f"[gpu] bad target {bad} v={v} in place", flush=True)
+        t = torch.randint(0, v, (n,), device=DEV, generator=g)
+        t[n // 2] = bad
+        anchor = torch.zeros((), device=DEV, requires_grad=True)
+        logits = x.clone() + anchor.to(torch.bfloat16)
+        with pytest.raises(ValueError, match="target token id is outside the model vocabulary"):
+            nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, inplace=True)
+        torch.cuda.synchronize()
+        assert torch.equal(logits.detach().view(torch.int16), x.view(torch.int16)), bad
+    t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    hint = torch.ones(1, dtype=torch.float32, device=DEV)
+    leaf = x.clone().requires_grad_(True)
+    ref = nmce.vocab_parallel_cross_entropy(leaf, t, 0, v, ctx, one_pass=False)
+    ref.backward()
+    anchor = torch.zeros((), device=DEV, requires_grad=True)
+    logits = x.clone() + anchor.to(torch.bfloat16)
+    got = []
+    logits.register_hook(lambda gr: got.append(gr))
+    loss = nmce.vocab_parallel_cross_entropy(logits, t, 0, v, ctx, inplace=True,
+                                             upstream_hint=hint)
+    loss.backward()
+    assert loss.item() == ref.item()
+    assert torch.equal(got[0].view(torch.int16), leaf.grad.view(torch.int16))
 
 
 @pytest.mark.parametrize("dtype,v", [(torch.bfloat16, 65544), (torch.bfloat16, 128256),
@@ -1004,7 +1078,7 @@ def test_one_pass_wide_rows(dtype, v):
         loss2 = nmce.vocab_parallel_cross_entropy(leaf, t, 0, v, ctx, one_pass=False)
         (loss2 * upstream).backward()
         ref_grad = leaf.grad
-        for inplace in (False, None):
+        for inplace in (False, True):
             hint = torch.ones(1, dtype=torch.float32, device=DEV)
             anchor = torch.zeros((), device=DEV, requires_grad=True)
             logits = x.clone() + anchor.to(dtype)
@@ -1087,7 +1161,7 @@ def test_c2_full_size_one_pass():
         (loss2 * upstream).backward()
         ref_grad = leaf.grad.view(N, V)
         del leaf
-        for inplace in (False, None):
+        for inplace in (False, True):
             hint = torch.ones(1, dtype=torch.float32, device=DEV)
             anchor = torch.zeros((), device=DEV, requires_grad=True)
             logits = x.view(8, 2048, V).clone() + anchor.to(torch.bfloat16)
@@ -1098,7 +1172,7 @@ def test_c2_full_size_one_pass():
             (loss * upstream).backward()
             assert loss.item() == loss2.item()
             grad = got[0].view(N, V)
-            assert (grad.data_ptr() == logits.data_ptr()) == (inplace is None)
+            assert (grad.data_ptr() == logits.data_ptr()) == inplace
             assert torch.equal(grad.view(torch.int16), ref_grad.view(torch.int16)), \
                 (upstream, inplace)
             del logits, got, grad

@@ -121,12 +121,32 @@ def test_lmhead_workspace_layout(lib):
 
 
 def test_default_chunk_never_holds_full_logits(lib):
-    """With the default chunk each of the backward's two gradient buffers (dZ
-    and dZ^T of one chunk) stays under a third of the full [tokens, vocab]
-    logits at the fused workloads, and a chunk covering the shard gives the
-    one-chunk layout."""
+    """The drop-in's default one-pass path at the fused workloads (c4: 16384
+    tokens x 128256 rows, H 4096; c5: 16384 x 256000, H 3072) allocates no
+    buffer of the [tokens, V] logits' size: the workspace's one chunk-sized
+    buffer, P^T, holds a quarter of the tokens (4096), its largest buffer is
+    the fp32 dW accumulator [V, H] (a size set by H, not by the tokens), and
+    the whole workspace stays under the bf16 logits' size. The recomputing backward's default vocabulary chunk
+    keeps each of its two gradient buffers under a third of the logits."""
     import ctypes
+    from nmce import _lib as L
     from nmce import lmhead
+    buf = (ctypes.c_int64 * L.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
+    for n, h, v in ((16384, 4096, 128256), (16384, 3072, 256000)):
+        logits_bytes = n * v * 2  # the bf16 logits
+        chunk = lmhead.default_token_chunk(n, v)
+        assert chunk == 4096
+        assert lib.nmce_lmhead_ce_fused_layout(n, h, v, chunk, ctypes.addressof(buf)) == 0
+        total, got_chunk, n_chunks = buf[0], buf[1], buf[2]
+        off_pt, off_part, off_acc, off_dxp = buf[6], buf[7], buf[8], buf[9]
+        assert (got_chunk, n_chunks) == (4096, 4)
+        pt_bytes = off_part - off_pt
+        assert pt_bytes == ((v + 255) // 256 * 256) * 4096 * 2
+        assert 4 * pt_bytes <= logits_bytes + 4 * 256 * 4096 * 2
+        regions = [off_part - off_pt, off_acc - off_part, off_dxp - off_acc, total - off_dxp]
+        assert max(regions) == off_dxp - off_acc and max(regions) <= logits_bytes / 2
+        assert total < logits_bytes
+        assert off_dxp - off_acc == (v * h * 4 + 255) // 256 * 256  # fp32 dW accumulator
     buf = (ctypes.c_int64 * 10)()
     for n, h, v in ((16384, 4096, 128256), (16384, 3072, 256000)):
         assert lib.nmce_lmhead_ce_bwd_layout(n, h, v, lmhead.DEFAULT_VOCAB_CHUNK,
@@ -138,33 +158,55 @@ def test_default_chunk_never_holds_full_logits(lib):
 
 
 def test_one_pass_token_chunk_budget(lib):
-    """The one-pass path's default token chunk: every token while the chunk's
-    exponentials, dZ^T once rescaled (2 V bytes per token), fit the budget, else the most
-    multiples of 256 that do; the fused layout then holds one chunk (no fp32
-    dW accumulator) or several (with one)."""
+    """The one-pass path's default token chunk: a quarter of the tokens rounded
+    up to 256 (at least 256; all of them up to 256), and no more than fit
+    CHUNK_BUDGET_BYTES of exponentials (2 V bytes per token); the fused layout
+    then holds one chunk (no fp32 dW accumulator) or several (with one). A
+    chunk of every token is the explicit opt-in with P^T the logits' size."""
     import ctypes
     from nmce import _lib as L
     from nmce import lmhead
     budget = lmhead.CHUNK_BUDGET_BYTES
     chunk = lmhead.default_token_chunk
-    assert chunk(16384, 128256) == 16384 and chunk(16384, 256000) == 16384
+    assert chunk(16384, 128256) == 4096 and chunk(16384, 256000) == 4096
+    assert chunk(1000, 5000) == 256 and chunk(256, 1000) == 256 and chunk(100, 1000) == 100
     for n, v in ((65536, 256000), (1 << 20, 128256), (40000, 1000000)):
         c = chunk(n, v)
-        assert c < n and c % 256 == 0
-        assert 2 * v * c <= budget < 2 * v * (c + 256)
-    assert chunk(100, 1 << 40) == 256  # at least one tile column
+        assert c < n and c % 256 == 0 and 4 * c <= n + 1024
+        assert 2 * v * c <= budget
+    assert chunk(100000, 1 << 40) == 256  # at least one tile column
     buf = (ctypes.c_int64 * L.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
-    # fields: total, chunk, n_chunks, ldt, vpad, nb, off_pt, off_part, off_acc
-    assert lib.nmce_lmhead_ce_fused_layout(16384, 4096, 128256, chunk(16384, 128256),
+    # fields: total, chunk, n_chunks, ldt, vpad, nb, off_pt, off_part, off_acc, off_dxp,
+    # dx_splits
+    assert lib.nmce_lmhead_ce_fused_layout(16384, 4096, 128256, 16384,
                                            ctypes.addressof(buf)) == 0
-    assert (buf[1], buf[2]) == (16384, 1) and buf[8] == buf[0]  # no accumulator region
+    assert (buf[1], buf[2]) == (16384, 1) and buf[8] == buf[9] == buf[0]  # no accumulator
     # P^T [vpad, ldt] bf16 is the only chunk-sized buffer: no transposed copies
     assert buf[7] - buf[6] == 128256 * 16384 * 2
     n, v = 65536, 256000
     assert lib.nmce_lmhead_ce_fused_layout(n, 3072, v, chunk(n, v), ctypes.addressof(buf)) == 0
-    assert buf[2] > 1 and buf[0] - buf[8] >= v * 3072 * 4  # fp32 dW accumulator
-    regions = [buf[6], buf[7], buf[8]]
+    assert buf[2] > 1 and buf[9] - buf[8] >= v * 3072 * 4  # fp32 dW accumulator
+    regions = [buf[6], buf[7], buf[8], buf[9], buf[0]]
     assert all(r % 256 == 0 for r in regions) and regions == sorted(regions)
+
+
+def test_fused_dx_split_choice(lib):
+    """A chunk's dX product (tokens x H tiles, K = the padded vocabulary) is
+    split over K when its 256x256 tiles leave compute units idle; the fp32
+    partials region holds every range. On a device with 256 compute units (the
+    choice depends on the current device; this host has none, so the query's
+    fallback of 256 applies): 4096 tokens x 4096 fill one round unsplit,
+    4096 x 3072 (192 tiles) take 4 ranges of 64000, 2048 x 3072 take 8."""
+    import ctypes
+    from nmce import _lib as L
+    buf = (ctypes.c_int64 * L.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
+    for n, h, v, ch, splits in ((16384, 4096, 128256, 4096, 1), (16384, 3072, 256000, 4096, 4),
+                                (16384, 3072, 256000, 2048, 8), (16384, 3072, 256000, 16384, 1),
+                                (300, 128, 777, 256, 1)):
+        assert lib.nmce_lmhead_ce_fused_layout(n, h, v, ch, ctypes.addressof(buf)) == 0
+        assert buf[10] == splits, (n, h, v, ch, buf[10])
+        want = (splits * ch * h * 4 + 255) // 256 * 256 if splits > 1 else 0
+        assert buf[0] - buf[9] == want
 
 
 def test_validate_slots(lib):

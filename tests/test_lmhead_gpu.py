@@ -291,8 +291,8 @@ def test_bwd_dz_buffers():
     one bf16 rounding (2^-8 relative, 2^-7 where the fp32 and fp64 values
     round to neighbours at a tie), dZ^T bit-for-bit its transpose, and the
     padding (rows past the shard, tokens past N) exactly zero."""
+    import ctypes
     from nmce import _lib as L
-    from nmce import lmhead as LH
     lib = L.load()
     n, h, v, chunk = 300, 128, 1000, 512
     x, w, t = make_inputs(n, h, v, seed=31, x_std=1.0, w_std=0.3)
@@ -313,8 +313,15 @@ def test_bwd_dz_buffers():
     L.check(lib.nmce_ce_combine(b, b + 4 * n, b + 8 * n, 1, 3 * n, n, out[0].data_ptr(),
                                 out[1].data_ptr(), out[2].data_ptr(), stream), "combine")
     go = g.float().to(DEV)
-    lay = LH._bwd_layout(lib, n, h, v, chunk)
+    buf = (ctypes.c_int64 * L.NMCE_LMHEAD_LAYOUT_FIELDS)()
+    L.check(lib.nmce_lmhead_ce_bwd_layout(n, h, v, chunk, ctypes.addressof(buf)), "layout")
+    lay = dict(zip(("total", "ldt", "vpad", "chunk", "n_chunks", "off_xt", "off_wt", "off_dzt",
+                    "off_dz", "off_acc"), (int(b) for b in buf)))
     ldt = lay["ldt"]
+
+    def bf16_view(offset, rows, cols):
+        return ws[offset:offset + rows * cols * 2].view(torch.bfloat16).view(rows, cols)
+
     assert lay["n_chunks"] == 2 and ldt == 320
     ws = torch.zeros(lay["total"], dtype=torch.uint8, device=DEV)
     L.check(lib.nmce_lmhead_ce_bwd_prepare(xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, v,
@@ -331,8 +338,8 @@ def test_bwd_dz_buffers():
         v0 = c * chunk
         mvalid = min(chunk, v - v0)
         mpad = (mvalid + 255) // 256 * 256
-        dz = LH._bf16_view(ws, lay["off_dz"], n, chunk)
-        dzt = LH._bf16_view(ws, lay["off_dzt"], chunk, ldt)
+        dz = bf16_view(lay["off_dz"], n, chunk)
+        dzt = bf16_view(lay["off_dzt"], chunk, ldt)
         got = dz[:, :mvalid].double().cpu().numpy()
         want = ref[:, v0:v0 + mvalid]
         bound = 2.0 ** -7 * np.abs(want) + 1e-30
@@ -394,31 +401,24 @@ def test_fused_two_shards_combined(v, chunk):
     check_grad(dxs[0] + dxs[1], rdx, "dH (sum of shards)")
 
 
-@pytest.mark.parametrize("route", ["library", "nmce"])
 @pytest.mark.parametrize("chunk", [256, 768, None])
-def test_dropin_backward_routes(route, chunk):
-    """The drop-in's recomputing backward (one_pass=False) through either GEMM
-    route (library GEMMs on the prepared buffers, or libnmce's own) against
-    the fp64 closed form."""
+def test_dropin_recomputing_backward(chunk):
+    """The drop-in's recomputing backward (one_pass=False: libnmce's dZ kernel
+    and its own GEMM for both products, dX accumulated in fp32 over the
+    vocabulary chunks) against the fp64 closed form."""
     import nmce
-    import nmce.lmhead as LH
     n, h, v = 320, 128, 1900
     x, w, t = make_inputs(n, h, v, seed=17, w_std=0.5)
-    saved = LH.BACKWARD_GEMM
-    LH.BACKWARD_GEMM = route
-    try:
-        xd = x.to(DEV).requires_grad_(True)
-        wd = w.to(DEV).requires_grad_(True)
-        loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v,
-                                                        nmce.ParallelContext.single(),
-                                                        vocab_chunk=chunk, one_pass=False)
-        loss.backward()
-    finally:
-        LH.BACKWARD_GEMM = saved
+    xd = x.to(DEV).requires_grad_(True)
+    wd = w.to(DEV).requires_grad_(True)
+    loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t.to(DEV), 0, v,
+                                                    nmce.ParallelContext.single(),
+                                                    vocab_chunk=chunk, one_pass=False)
+    loss.backward()
     rl, _, rdx, rdw = fp64_reference(x, w, t)
     assert abs(loss.item() - rl.mean()) <= 1e-5 * abs(rl.mean())
-    check_grad(xd.grad.float().cpu().numpy(), rdx, f"dH ({route}, chunk {chunk})")
-    check_grad(wd.grad.float().cpu().numpy(), rdw, f"dW ({route}, chunk {chunk})")
+    check_grad(xd.grad.float().cpu().numpy(), rdx, f"dH (chunk {chunk})")
+    check_grad(wd.grad.float().cpu().numpy(), rdw, f"dW (chunk {chunk})")
 
 
 @pytest.mark.parametrize("v", [1024, 640, 600])
@@ -651,21 +651,18 @@ def _lse_all(xd, wd, chunk=1024):
     return torch.cat(out)
 
 
-@pytest.mark.parametrize("route", ["one_pass", "one_pass_chunked", "library", "nmce"])
+@pytest.mark.parametrize("route", ["one_pass", "one_pass_one_chunk", "recompute"])
 @pytest.mark.parametrize("cfg", ["c4", "c5"])
-def test_fused_workload(cfg, route, monkeypatch):
+def test_fused_workload(cfg, route):
     """c4: hidden [16384, 4096] ~ N(0,1), W [128256, 4096] ~ N(0, 0.02^2), uniform
     targets. c5: hidden [16384, 3072], W [256000, 3072] ~ N(0, 0.05^2) with 64
     rows x30, Zipf(1.1) targets (logits far beyond +-60). Every route: the
-    drop-in's default one-pass path (one chunk of all 16384 tokens; the mean
-    loss equal to the per-token Function's, bit for bit), the same in two
-    chunks of 8192 tokens (dW accumulated in fp32 across them), and the
-    recomputing backward through the library's products or the hand-written
-    one (dX accumulated in fp32 over the 32768-row vocabulary chunks, 4 at c4,
-    8 at c5)."""
+    drop-in's default one-pass path (bounded token chunks, dW accumulated in
+    fp32 across them; the mean loss equal to the per-token Function's, bit for
+    bit), the same as one chunk of all 16384 tokens (the opt-in that holds the
+    exponentials of every token), and the recomputing backward (dX accumulated
+    in fp32 over the 32768-row vocabulary chunks, 4 at c4, 8 at c5)."""
     import nmce
-    from nmce import lmhead as lm
-    monkeypatch.setattr(lm, "BACKWARD_GEMM", route)
     g = torch.Generator(device=DEV).manual_seed(0)
     if cfg == "c4":
         n, h, v = 16384, 4096, 128256
@@ -688,7 +685,7 @@ def test_fused_workload(cfg, route, monkeypatch):
     wd = w.clone().requires_grad_(True)
     if route.startswith("one_pass"):
         hint = torch.ones(1, dtype=torch.float32, device=DEV)
-        chunk = 8192 if route == "one_pass_chunked" else None
+        chunk = n if route == "one_pass_one_chunk" else None
         loss = nmce.lmhead_vocab_parallel_cross_entropy(xd, wd, t, 0, v, ctx,
                                                         token_chunk=chunk, upstream_hint=hint)
         loss.backward()
@@ -732,12 +729,16 @@ def test_fused_workload(cfg, route, monkeypatch):
 
 @pytest.mark.parametrize("n,h,v,chunk", [(300, 128, 777, None), (1000, 192, 1900, 256),
                                          (513, 100, 3001, 256), (64, 64, 1, None),
-                                         (700, 64, 129, 512), (2048, 256, 20000, 768)])
+                                         (700, 64, 129, 512), (2048, 256, 20000, 768),
+                                         (1100, 320, 7800, 256)])
 def test_one_pass_fused_against_oracle(n, h, v, chunk):
     """The drop-in's one-pass forward (dX and dW formed chunk by chunk over the
     tokens, for the assumed upstream 1.0) against the fp64 closed form: one
     chunk, several with a short last one, a hidden size padded to 64, a
-    vocabulary of one row and one that ends a row into a 128-row block."""
+    vocabulary of one row and one that ends a row into a 128-row block. The
+    last two split a chunk's dX product over K (its tiles are too few for the
+    device): 8 equal ranges at V = 20000, and 3 at V = 7800 with a shorter last
+    range and a hidden size of 320 (a 64-column edge tile)."""
     import nmce
     print(f"[gpu] one-pass fused n={n} h={h} v={v} chunk={chunk}", flush=True)
     x, w, t = make_inputs(n, h, v, seed=n + v, w_std=0.5)

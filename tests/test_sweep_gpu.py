@@ -412,7 +412,7 @@ def test_one_pass_sweep(case):
     L.check(lib.nmce_ce_fwd_bwd(work.data_ptr(), grad.data_ptr(), code, n, v, ld, ldg,
                                 t.data_ptr(), out[0].data_ptr(), out[1].data_ptr(),
                                 out[2].data_ptr(), expect.data_ptr(), assumed.data_ptr(),
-                                float(n), stream), "fwd_bwd")
+                                None, float(n), stream), "fwd_bwd")
     torch.cuda.synchronize()
     a = assumed.item()
     usable = math.isfinite(hint) and abs(hint) >= 1.17549435e-38
