@@ -32,12 +32,24 @@
 namespace nmce {
 namespace {
 
+// Launch shapes (overridable at build time for sweeps; the fold order of the
+// statistics kernel, and so its bits, depends on NMCE_STATS_UNROLL, the flat
+// backward's results do not depend on its shape).
+#ifndef NMCE_STATS_UNROLL
+#define NMCE_STATS_UNROLL 2
+#endif
+#ifndef NMCE_FLAT_BLOCK
+#define NMCE_FLAT_BLOCK 128
+#endif
+#ifndef NMCE_FLAT_UNROLL
+#define NMCE_FLAT_UNROLL 2
+#endif
 constexpr int kStatsBlock = 1024;
-constexpr int kStatsUnroll = 2;
+constexpr int kStatsUnroll = NMCE_STATS_UNROLL;
 constexpr int kBwdBlock = 1024;   // row-per-workgroup backward
 constexpr int kBwdUnroll = 4;
-constexpr int kFlatBlock = 128;   // flat backward
-constexpr int kFlatUnroll = 2;
+constexpr int kFlatBlock = NMCE_FLAT_BLOCK;   // flat backward
+constexpr int kFlatUnroll = NMCE_FLAT_UNROLL;
 constexpr int kValidateThreads = 256;
 // Running maxima start here instead of -inf so that rows (or lanes) that have
 // seen only -inf keep finite shifts and 2^(x-m) stays 0 rather than NaN.
@@ -748,9 +760,16 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
 // differs from the assumed[0] the gradient was written for, every entry is
 // scaled by gout[0] / assumed[0] (each is linear in the upstream value:
 // cross_entropy.py:64). Rows as in the one-pass kernel (16-byte aligned, V a
-// whole number of vectors), walked by two workgroups per compute unit, so that
-// a hit costs one short launch. gout[0] also goes to observed[0] for the next forward.
-template <typename T, int kBlock = kBwdBlock, int kUnroll = kBwdUnroll>
+// whole number of vectors). Two workgroups per compute unit, so that a hit
+// costs one short launch; on a miss they stream the slab's vectors in one
+// grid-stride sweep (rows concatenated when they are contiguous), kUnroll
+// vectors in flight per lane. Measured on [16384, 50304] bf16: 256 lanes x 2
+// vectors per workgroup, 0.56 ms; 1024 x 4, 0.64 ms (more waves in flight
+// spread the sweep over more of HBM at once). gout[0] also goes to
+// observed[0] for the next forward.
+constexpr int kRescaleBlock = 256;
+constexpr int kRescaleUnroll = 2;
+template <typename T, int kBlock = kRescaleBlock, int kUnroll = kRescaleUnroll>
 __global__ __launch_bounds__(kBlock) void ce_grad_rescale_kernel(
     T* g, int64_t n_rows, int64_t V, int64_t ldg, const float* __restrict__ gout,
     const float* __restrict__ assumed, float* __restrict__ observed) {
@@ -761,23 +780,33 @@ __global__ __launch_bounds__(kBlock) void ce_grad_rescale_kernel(
   const float a = assumed[0];
   if (gv == a) return;
   const float ratio = gv / a;
-  const int64_t nvec = V / EPV;
-  for (int64_t row = blockIdx.x; row < n_rows; row += gridDim.x) {
-    u32x4* gr = reinterpret_cast<u32x4*>(g + row * ldg);
-    for (int64_t i0 = threadIdx.x; i0 < nvec; i0 += kUnroll * kBlock) {
-      u32x4 v[kUnroll];
+  // Vector f of the slab: f * EPV elements in when the rows are contiguous;
+  // otherwise (row, col) = (f / vpr, f % vpr), by 32-bit division when the
+  // slab has fewer than 2^32 vectors.
+  const bool flat = ldg == V;
+  const uint64_t vpr = V / EPV;
+  const uint64_t total = static_cast<uint64_t>(n_rows) * vpr;
+  const bool narrow = total < (uint64_t{1} << 32);
+  const uint64_t stride = static_cast<uint64_t>(gridDim.x) * kBlock;
+  auto at = [&](uint64_t f) {
+    if (flat) return reinterpret_cast<u32x4*>(g + f * EPV);
+    const uint64_t r = narrow ? static_cast<uint32_t>(f) / static_cast<uint32_t>(vpr) : f / vpr;
+    return reinterpret_cast<u32x4*>(g + r * ldg + (f - r * vpr) * EPV);
+  };
+  for (uint64_t f0 = static_cast<uint64_t>(blockIdx.x) * kBlock + threadIdx.x; f0 < total;
+       f0 += stride * kUnroll) {
+    u32x4 v[kUnroll];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u)
-        if (i0 + u * kBlock < nvec) v[u] = load_stream(gr + i0 + u * kBlock);
+    for (int u = 0; u < kUnroll; ++u)
+      if (f0 + u * stride < total) v[u] = load_stream(at(f0 + u * stride));
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) {
-        if (i0 + u * kBlock < nvec) {
-          float f[EPV];
-          E::unpack(v[u], f);
+    for (int u = 0; u < kUnroll; ++u) {
+      if (f0 + u * stride < total) {
+        float f[EPV];
+        E::unpack(v[u], f);
 #pragma unroll
-          for (int k = 0; k < EPV; ++k) f[k] *= ratio;
-          store_stream(gr + i0 + u * kBlock, E::pack(f));
-        }
+        for (int k = 0; k < EPV; ++k) f[k] *= ratio;
+        store_stream(at(f0 + u * stride), E::pack(f));
       }
     }
   }
@@ -1157,7 +1186,7 @@ int nmce_ce_grad_rescale_unless(void* grad, int dtype, int64_t n_rows, int64_t v
   if (!grad || !grad_output || !assumed) return NMCE_EINVAL_PTR;
   if (reinterpret_cast<uintptr_t>(grad) % 16 || (ld_grad * es) % 16) return NMCE_EINVAL_ALIGN;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  const dim3 grid(after_one_pass_grid(n_rows)), block(kBwdBlock);
+  const dim3 grid(after_one_pass_grid(n_rows)), block(kRescaleBlock);
   if (dtype == NMCE_F32)
     hipLaunchKernelGGL(ce_grad_rescale_kernel<float>, grid, block, 0, st,
                        static_cast<float*>(grad), n_rows, vocab, ld_grad, grad_output, assumed,

@@ -221,6 +221,23 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return stream
 
 
+# Per (device, stream): the device word the one-workgroup target check writes
+# and the one-pass kernel reads. Both run on that stream, one after the
+# other, so calls on one stream can share it; calls on other streams have
+# their own.
+_flag_words: dict[tuple, torch.Tensor] = {}
+
+
+def _flag_word(device: torch.device, stream: int) -> torch.Tensor:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (idx, stream)
+    word = _flag_words.get(key)
+    if word is None:
+        word = torch.empty(1, dtype=torch.int32, device=device)
+        _flag_words[key] = word
+    return word
+
+
 def launch_target_check(target: torch.Tensor, vocab_size: int,
                         on_side_stream: bool = True,
                         device_flag: torch.Tensor | None = None) -> _PendingCheck | None:
@@ -406,8 +423,7 @@ def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint
     into a new buffer. Returns the flat per-token loss; the backward keeps that
     gradient unless its upstream value differs. ``bad_flag``: the device count
     of the target check enqueued just before; the kernel writes nothing when
-    it is nonzero."""
-    _check_inputs(logits, target, vocab_start, vocab_end)
+    it is nonzero. Only the wrapper calls it, after checking the inputs."""
     lib = _lib.load()
     dev = logits.device
     n, V = rows.shape
@@ -642,7 +658,7 @@ def vocab_parallel_cross_entropy(
     bad_flag = None
     if validate and hint is not None:
         # the one-pass kernel reads the check's count before writing anything
-        bad_flag = torch.empty(1, dtype=torch.int32, device=logits.device)
+        bad_flag = _flag_word(logits.device, _lib.stream_handle(logits.device))
     pending = (launch_target_check(target, vocab_size, on_side_stream=hint is None,
                                    device_flag=bad_flag)
                if validate else None)
