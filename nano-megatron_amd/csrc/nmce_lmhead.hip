@@ -2,8 +2,9 @@
 //
 // Replaces ParallelLMHead's projection Z = X @ W^T (nano_megatron/model.py:192,
 // run in bf16 under autocast, model.py:255-257) followed by the loss of
-// nano_megatron/cross_entropy.py:16-65, without ever holding Z for the whole
-// vocabulary.
+// nano_megatron/cross_entropy.py:16-65, without ever holding Z (or anything of
+// its size) for every token: at most one chunk of tokens' exponentials, or one
+// vocabulary chunk's gradient, at a time.
 //
 // Every product is one bf16 GEMM core, C[m, n] = sum_k A[m, k] * B[n, k] on
 // v_mfma_f32_32x32x16_bf16, each operand K-contiguous or MN-contiguous
@@ -11,7 +12,8 @@
 //
 //   forward   Z^T = W X^T    (M = vocab, N = tokens, K = hidden). The epilogue
 //             reduces each 128-row vocabulary block of a token's column to a
-//             partial (max, sum exp, target logit); Z is never stored.
+//             partial (max, sum exp, target logit); this statistics-only form
+//             stores nothing of Z.
 //   backward  per vocabulary chunk of Vc rows:
 //             dZ^T_c = recompute(W_c X^T) -> (softmax - onehot) * g, written as
 //                      bf16 in both layouts [Vc, tokens] and [tokens, Vc]
@@ -19,12 +21,13 @@
 //             dX    += dZ_c W_c      (M = tokens, N = hidden, K = Vc; B = W^T)
 //
 // The one-pass path (the drop-in's default) computes Z once, per chunk of
-// tokens (all of them when the chunk's buffer fits the caller's budget):
+// tokens (the caller's choice; the drop-in takes a quarter of the tokens):
 //             P^T  = exp(W X^T - block max), bf16, with the partial statistics
 //             dZ^T = P^T * exp(block max - M) * g / S - onehot, in place
 //                    (once the statistics are combined)
 //             dX   = dZ W            (K = vocab; dZ^T and W both read
-//                                     vocabulary-row major, as they lie)
+//                                     vocabulary-row major, as they lie; split
+//                                     over K when the chunk's tiles are few)
 //             dW  += dZ^T X          (K = the chunk's tokens; X read token-row
 //                                     major, as it lies; fp32 across chunks
 //                                     only when there are several)
