@@ -314,20 +314,36 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
     bf16x8_t a[kFM];
     bf16x8_t b[kFN];
   };
+  auto read_a = [&](const char* st, int s, Frags& f, int i) {
+    if constexpr (kAMN)
+      f.a[i] = read_tr(st + 16 * s * 512, a_tr[i]);
+    else
+      f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
+  };
+  auto read_b = [&](const char* st, int s, Frags& f, int j) {
+    if constexpr (kBMN)
+      f.b[j] = read_tr(st + 16 * s * 512, b_tr[j]);
+    else
+      f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
+  };
   auto load_frags = [&](const char* st, int s, Frags& f) {
+    if constexpr (kAMN || kBMN) {
+      // In the order the MFMAs first use them (B0 A0, B1, A1, A2, ...), so
+      // that each MFMA of the next sub-step waits only for its own reads:
+      // +3% on the product with both operands MN-contiguous (two transposing
+      // reads per fragment), +0.3% with one; -0.4% with none, which keeps
+      // the A-first order.
+      constexpr int kMax = kFM > kFN ? kFM : kFN;
 #pragma unroll
-    for (int i = 0; i < kFM; ++i) {
-      if constexpr (kAMN)
-        f.a[i] = read_tr(st + 16 * s * 512, a_tr[i]);
-      else
-        f.a[i] = *reinterpret_cast<const bf16x8_t*>(st + a_row_off + i * 32 * 128 + xo[s]);
-    }
+      for (int i = 0; i < kMax; ++i) {
+        if (i < kFN) read_b(st, s, f, i);
+        if (i < kFM) read_a(st, s, f, i);
+      }
+    } else {
 #pragma unroll
-    for (int j = 0; j < kFN; ++j) {
-      if constexpr (kBMN)
-        f.b[j] = read_tr(st + 16 * s * 512, b_tr[j]);
-      else
-        f.b[j] = *reinterpret_cast<const bf16x8_t*>(st + b_row_off + j * 32 * 128 + xo[s]);
+      for (int i = 0; i < kFM; ++i) read_a(st, s, f, i);
+#pragma unroll
+      for (int j = 0; j < kFN; ++j) read_b(st, s, f, j);
     }
   };
   auto mma = [&](const Frags& f) {
