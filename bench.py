@@ -2,6 +2,7 @@
 """Benchmark of the vocabulary-parallel cross entropy on one MI355X.
 
     python bench.py [--steps K] [--warmup W] [--workload c1..c5 [--two-pass]] [--gpus 1]
+    python bench.py --gemm-core     (the fused path's GEMM core beside hipBLASLt)
 
 Unfused workloads (c1-c3): a step is one forward + backward of the loss over
 one batch of synthetic logits already resident in HBM, through the drop-in
@@ -144,7 +145,60 @@ def parse_args():
                    help="unfused: device memory for the per-step copies of the logits")
     p.add_argument("--detail", default=None,
                    help="also write every measured field to this JSON file")
+    p.add_argument("--gemm-core", action="store_true",
+                   help="instead: time the fused path's GEMM core beside torch.mm "
+                        "(hipBLASLt) on the c4 forward product's shape, one JSON line")
     return p.parse_args()
+
+
+def run_gemm_core(reps: int = 8, rounds: int = 3) -> dict:
+    """The fused path's bf16 GEMM core (nmce_gemm_nt_bf16, the main loop of
+    all three fused products) beside torch.mm, which dispatches to hipBLASLt,
+    on the c4 forward product's shape: C[V, C] = W[V, H] X_c[C, H]^T with
+    V = 128256, a chunk of C = 4096 tokens, H = 4096, W ~ N(0, 0.02^2) and
+    X ~ N(0, 1) as at c4 (the chip's clock under its power cap depends on the
+    data). Rounds of ``reps`` calls of each, interleaved; the best round each.
+    A reference point for the MFMA roofline; nothing of the loss runs."""
+    import torch
+    from nmce import _lib as L
+
+    lib = L.load()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    M, N, K = 128256, 4096, 4096
+    gen = torch.Generator(device=dev).manual_seed(0)
+    a = (torch.randn(M, K, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+    b = torch.randn(N, K, device=dev, generator=gen).to(torch.bfloat16)
+    c_own = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+    c_lib = torch.empty_like(c_own)
+    stream = L.stream_handle(dev)
+
+    def own():
+        L.check(lib.nmce_gemm_nt_bf16(a.data_ptr(), K, b.data_ptr(), K, M, N, K,
+                                      c_own.data_ptr(), L.NMCE_BF16, N, stream), "gemm")
+
+    def blas():
+        torch.mm(a, b.t(), out=c_lib)
+
+    flop = 2.0 * M * N * K
+    best = {"nmce_gemm_nt_bf16": float("inf"), "torch.mm (hipBLASLt)": float("inf")}
+    for _ in range(rounds):
+        for name, fn in (("nmce_gemm_nt_bf16", own), ("torch.mm (hipBLASLt)", blas)):
+            fn()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            best[name] = min(best[name], e0.elapsed_time(e1) / reps)
+    out = {"metric": "bf16 GEMM TFLOP/s, C[128256,4096] = A[128256,4096] B[4096,4096]^T",
+           "shape_mnk": [M, N, K], "peak_tflops": MFMA_BF16_PEAK_TFLOPS}
+    for name, ms in best.items():
+        tf = flop / ms / 1e9
+        out[name] = {"ms": ms, "tflops": tf, "frac": tf / MFMA_BF16_PEAK_TFLOPS}
+    out["max_abs_diff"] = (c_own.float() - c_lib.float()).abs().max().item()
+    return out
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_ce.json"
@@ -652,6 +706,10 @@ def main() -> int:
                           "(the TP exchange is one all-gather of [3, tokens] statistics, "
                           "not exercised here)"}))
         return 2
+
+    if args.gemm_core:
+        print(json.dumps(_round(run_gemm_core()), separators=(",", ":")), flush=True)
+        return 0
 
     with_cpu = not args.no_cpu_baseline
     details = {}

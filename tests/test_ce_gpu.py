@@ -1192,6 +1192,55 @@ def test_c2_full_size_one_pass():
     torch.cuda.empty_cache()
 
 
+def test_wide_full_size_one_pass():
+    """The wide-row workload the benchmark times, bf16 [4,2048,128256] ~ N(0,1)
+    at TP = 1: the one-pass kernel that keeps part of each row in LDS walks
+    8192 rows, 32 per workgroup on 256 compute units, with the next row's loads
+    in flight. In place and into a separate buffer, at upstream 1.0 and 0.5,
+    bit for bit against the two-pass path on the whole slab; the loss against a
+    chunked fp64 reference; sampled gradient rows against the oracle."""
+    import nmce
+    print("[gpu] wide one-pass bf16 [4,2048,128256]", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    N, V = 4 * 2048, 128256
+    x = torch.randn(N, V, device=DEV, generator=gen).to(torch.bfloat16)
+    t = torch.randint(0, V, (N,), device=DEV, generator=gen)
+    ctx = nmce.ParallelContext.single()
+    tv = t.view(4, 2048)
+    for upstream in (1.0, 0.5):
+        leaf = x.view(4, 2048, V).clone().requires_grad_(True)
+        loss2 = nmce.vocab_parallel_cross_entropy(leaf, tv, 0, V, ctx, one_pass=False)
+        (loss2 * upstream).backward()
+        ref_grad = leaf.grad.view(N, V)
+        del leaf
+        for inplace in (False, True):
+            hint = torch.ones(1, dtype=torch.float32, device=DEV)
+            anchor = torch.zeros((), device=DEV, requires_grad=True)
+            logits = x.view(4, 2048, V).clone() + anchor.to(torch.bfloat16)
+            got = []
+            logits.register_hook(lambda gr: got.append(gr))
+            loss = nmce.vocab_parallel_cross_entropy(logits, tv, 0, V, ctx, inplace=inplace,
+                                                     upstream_hint=hint)
+            (loss * upstream).backward()
+            assert loss.item() == loss2.item()
+            grad = got[0].view(N, V)
+            assert (grad.data_ptr() == logits.data_ptr()) == inplace
+            assert torch.equal(grad.view(torch.int16), ref_grad.view(torch.int16)), \
+                (upstream, inplace)
+            del logits, got, grad
+        if upstream == 1.0:
+            ref_loss = _torch_ref_rows(x, t)
+            assert abs(loss2.item() - ref_loss.mean().item()) <= 1e-6 * abs(
+                ref_loss.mean().item())
+            pick = torch.arange(0, N, 1021, device=DEV)
+            _, og = ce_oracle.closed_form(x[pick].float().cpu().numpy(), t[pick].cpu().numpy(),
+                                          1.0 / N)
+            assert_bf16_close(ref_grad[pick].float().cpu().numpy(), og, what="wide grad rows",
+                              atol=1e-30)
+        del ref_grad
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_one_pass_extreme_rows(dtype):
     """The one-pass path against the two-pass path, bit for bit, on rows at the
