@@ -354,22 +354,31 @@ def cpu_baseline_fused(wl: dict, seconds: float, rows: int = 128) -> dict:
 def _kernel_times(run_steps, steps: int):
     """Average duration per launch of each libnmce entry over ``steps`` more
     steps (``run_steps(k)`` runs k of them), from HIP event pairs recorded on
-    the launch stream around every launch (nmce.cross_entropy.kernel_timeline).
-    Event records add small gaps between launches, so this region's wall time
-    is not the step time. Returns ({name: ms}, {name: launches})."""
+    the launch stream around every launch: the Python host layer's
+    (nmce.cross_entropy.kernel_timeline) and the one-pass autograd node's
+    (``_nmce_autograd.set_timing``). Event records add small gaps between
+    launches, so this region's wall time is not the step time. Returns
+    ({name: ms}, {name: launches})."""
     import torch
     import nmce.cross_entropy as ce_mod
+    from nmce import _lib
 
+    ext = _lib.autograd_ext()
+    ext.take_timeline()
     timeline: list = []
     ce_mod.kernel_timeline = timeline
+    ext.set_timing(True)
     try:
         run_steps(steps)
         torch.cuda.synchronize()
     finally:
         ce_mod.kernel_timeline = None
+        ext.set_timing(False)
     per: dict[str, list[float]] = {}
     for name, s_ev, e_ev in timeline:
         per.setdefault(name, []).append(s_ev.elapsed_time(e_ev))
+    for name, ms in ext.take_timeline():
+        per.setdefault(name, []).append(ms)
     return ({k: sum(vs) / len(vs) for k, vs in per.items()},
             {k: len(vs) for k, vs in per.items()})
 

@@ -1,0 +1,242 @@
+// The drop-in loss's one-pass path at TP = 1 as a C++ autograd node.
+//
+// Forward and backward of cross_entropy.py:16-65 followed by the wrapper's
+// .mean() (:85), for the rows the one-pass kernel takes: one launch of
+// nmce_ce_fwd_bwd writes the per-token loss, the row statistics and the
+// gradient of the mean for the assumed upstream value; the backward launches
+// nmce_ce_grad_rescale_unless (gradient in the logits' storage) or
+// nmce_ce_bwd_scaled_unless (a separate buffer), which leave it as it is when
+// the upstream value is the assumed one. Host code only: the kernels are
+// libnmce.so's, reached through its C ABI (include/nmce.h).
+//
+// A node written in Python costs the autograd engine a hand-over to the
+// interpreter on its device thread for every backward, and the forward's
+// Python bookkeeping besides: tens of microseconds per call, which a small
+// batch (a step of a few tens of microseconds of kernels) pays in full. The
+// Python wrapper still validates the arguments, resolves the upstream hint
+// and runs the target check; this node does the rest.
+#include <torch/extension.h>
+#include <torch/csrc/autograd/variable.h>
+#include <c10/hip/HIPStream.h>
+#include <hip/hip_runtime_api.h>
+
+#include <mutex>
+#include <string>
+#include <tuple>
+#include <vector>
+
+#include "nmce.h"
+
+namespace {
+
+using torch::autograd::AutogradContext;
+using torch::autograd::variable_list;
+
+void check(int status, const char* what) {
+  TORCH_CHECK(status == 0, "nmce: ", what, " failed with status ", status, ": ",
+              nmce_status_string(status));
+}
+
+int dtype_code(const at::Tensor& t) {
+  if (t.scalar_type() == at::kFloat) return NMCE_F32;
+  if (t.scalar_type() == at::kBFloat16) return NMCE_BF16;
+  TORCH_CHECK(false, "nmce: unsupported logits dtype ", t.scalar_type());
+}
+
+hipStream_t stream_of(const at::Tensor& t) {
+  return c10::hip::getCurrentHIPStream(t.device().index()).stream();
+}
+
+// Optional per-launch timing: HIP event pairs recorded on the launch stream
+// around every launch of this file while enabled, read back by
+// take_timeline() (the benchmark's per-call times).
+std::mutex g_timeline_lock;
+bool g_timing = false;
+std::vector<std::tuple<std::string, hipEvent_t, hipEvent_t>> g_timeline;
+
+template <typename Launch>
+void timed(const char* name, hipStream_t st, Launch&& launch) {
+  if (!g_timing) {
+    check(launch(), name);
+    return;
+  }
+  hipEvent_t a = nullptr, b = nullptr;
+  TORCH_CHECK(hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess,
+              "nmce: hipEventCreate failed");
+  TORCH_CHECK(hipEventRecord(a, st) == hipSuccess, "nmce: hipEventRecord failed");
+  const int status = launch();
+  TORCH_CHECK(hipEventRecord(b, st) == hipSuccess, "nmce: hipEventRecord failed");
+  {
+    std::lock_guard<std::mutex> g(g_timeline_lock);
+    g_timeline.emplace_back(name, a, b);
+  }
+  check(status, name);
+}
+
+struct OnePassMean : public torch::autograd::Function<OnePassMean> {
+  // logits [..., V] viewable as [rows, V] (16-byte aligned rows, V a whole
+  // number of 16-byte vectors within the kernel's width; the wrapper checked),
+  // target the flat contiguous int64 targets, hint the one-element fp32
+  // upstream value to assume, bad_flag the address of the target check's
+  // device word (0 without a check; not an autograd input), inplace whether
+  // the gradient goes into the logits' storage.
+  static at::Tensor forward(AutogradContext* ctx, const at::Tensor& logits,
+                            const at::Tensor& target, const at::Tensor& hint, int64_t bad_flag,
+                            bool inplace, int64_t vocab_start) {
+    const int64_t V = logits.size(-1);
+    const at::Tensor rows = logits.view({-1, V});
+    const int64_t n = rows.size(0);
+    const int64_t ld = n > 1 ? rows.stride(0) : V;
+    const int code = dtype_code(rows);
+    at::Tensor out = at::empty({3, n}, rows.options().dtype(at::kFloat));  // loss, max, sum - 1
+    at::Tensor loss = out.select(0, 0);
+    at::Tensor row_stat = out.slice(0, 1, 3);
+    at::Tensor grad = inplace ? rows : at::empty({n, V}, rows.options());
+    const int64_t ldg = inplace ? ld : V;
+    at::Tensor assumed = at::empty({1}, out.options());
+    hipStream_t st = stream_of(rows);
+    float* stats = out.data_ptr<float>();
+    timed("nmce_ce_fwd_bwd", st, [&] {
+      return nmce_ce_fwd_bwd(rows.data_ptr(), grad.data_ptr(), code, n, V, ld, ldg,
+                             target.data_ptr<int64_t>(), stats, stats + n, stats + 2 * n,
+                             hint.data_ptr<float>(), assumed.data_ptr<float>(),
+                             reinterpret_cast<const int32_t*>(bad_flag),
+                             static_cast<float>(n), st);
+    });
+    ctx->saved_data["inplace"] = inplace;
+    ctx->saved_data["ld"] = ld;
+    ctx->saved_data["vocab_start"] = vocab_start;
+    ctx->saved_data["handed_out"] = false;
+    ctx->saved_data["shape"] = logits.sizes().vec();
+    if (inplace) {
+      // The logits now hold the gradient: autograd nodes that saved them fail
+      // their version check rather than read it.
+      torch::autograd::impl::bump_version(logits);
+      ctx->saved_data["grad_buf"] = logits.detach();
+      ctx->save_for_backward({target, row_stat, assumed, hint});
+    } else {
+      ctx->save_for_backward({rows, target, row_stat, grad, assumed, hint});
+    }
+    return loss.mean();
+  }
+
+  static variable_list backward(AutogradContext* ctx, variable_list grad_outputs) {
+    at::Tensor go = grad_outputs[0].reshape({1});
+    if (go.scalar_type() != at::kFloat) go = go.to(at::kFloat);
+    go = go.contiguous();
+    const bool inplace = ctx->saved_data["inplace"].toBool();
+    const int64_t ld = ctx->saved_data["ld"].toInt();
+    const std::vector<int64_t> shape = ctx->saved_data["shape"].toIntVector();
+    const int64_t V = shape.back();
+    const variable_list saved = ctx->get_saved_variables();
+    variable_list grads(6);
+    if (inplace) {
+      TORCH_CHECK(!ctx->saved_data["handed_out"].toBool(),
+                  "nmce: a second backward through an in-place one-pass loss needs the logits, "
+                  "which now hold the gradient; pass inplace=False to differentiate it twice");
+      const at::Tensor& target = saved[0];
+      const at::Tensor& assumed = saved[2];
+      const at::Tensor& hint = saved[3];
+      at::Tensor grad = ctx->saved_data["grad_buf"].toTensor();
+      const int64_t n = target.numel();
+      hipStream_t st = stream_of(grad);
+      timed("nmce_ce_grad_rescale_unless", st, [&] {
+        return nmce_ce_grad_rescale_unless(grad.data_ptr(), dtype_code(grad), n, V, ld,
+                                           go.data_ptr<float>(), assumed.data_ptr<float>(),
+                                           hint.data_ptr<float>(), st);
+      });
+      ctx->saved_data["handed_out"] = true;
+      ctx->saved_data["grad_buf"] = at::Tensor();
+      grads[0] = grad;
+      return grads;
+    }
+    const at::Tensor& rows = saved[0];
+    const at::Tensor& target = saved[1];
+    const at::Tensor& row_stat = saved[2];
+    const at::Tensor& grad = saved[3];
+    const at::Tensor& assumed = saved[4];
+    const at::Tensor& hint = saved[5];
+    const int64_t n = rows.size(0);
+    const int64_t vocab_start = ctx->saved_data["vocab_start"].toInt();
+    const float gdiv = static_cast<float>(n > 1 ? n : 1);
+    hipStream_t st = stream_of(rows);
+    const float* stats = row_stat.data_ptr<float>();
+    if (ctx->saved_data["handed_out"].toBool()) {
+      // A second backward through the same graph: the first one's buffer
+      // belongs to its consumers; a new one from the logits.
+      at::Tensor fresh = at::empty({n, V}, rows.options());
+      timed("nmce_ce_bwd_scaled", st, [&] {
+        return nmce_ce_bwd_scaled(rows.data_ptr(), fresh.data_ptr(), dtype_code(rows), n, V, ld,
+                                  V, target.data_ptr<int64_t>(), vocab_start, stats, stats + n,
+                                  go.data_ptr<float>(), 0, gdiv, st);
+      });
+      grads[0] = fresh.view(shape);
+      return grads;
+    }
+    timed("nmce_ce_bwd_scaled_unless", st, [&] {
+      return nmce_ce_bwd_scaled_unless(rows.data_ptr(), grad.data_ptr(), dtype_code(rows), n, V,
+                                       ld, V, target.data_ptr<int64_t>(), vocab_start, stats,
+                                       stats + n, go.data_ptr<float>(), gdiv,
+                                       assumed.data_ptr<float>(), hint.data_ptr<float>(), st);
+    });
+    ctx->saved_data["handed_out"] = true;
+    grads[0] = grad.view(shape);
+    return grads;
+  }
+};
+
+at::Tensor one_pass_mean(const at::Tensor& logits, const at::Tensor& target,
+                         const at::Tensor& hint, const c10::optional<at::Tensor>& bad_flag,
+                         bool inplace, int64_t vocab_start) {
+  const int64_t flag = bad_flag.has_value() && bad_flag->defined()
+                           ? reinterpret_cast<int64_t>(bad_flag->data_ptr<int32_t>())
+                           : 0;
+  return OnePassMean::apply(logits, target, hint, flag, inplace, vocab_start);
+}
+
+// The assumed upstream value a one-pass loss's forward used, for tests that
+// follow which backward kept the forward's gradient: the saved fp32 word.
+at::Tensor assumed_of(const at::Tensor& loss) {
+  auto fn = loss.grad_fn();
+  TORCH_CHECK(fn, "nmce: not a one-pass loss");
+  auto* node = dynamic_cast<torch::autograd::CppNode<OnePassMean>*>(fn.get());
+  TORCH_CHECK(node, "nmce: not a one-pass loss");
+  const variable_list saved = node->ctx_.get_saved_variables();
+  return saved[node->ctx_.saved_data.at("inplace").toBool() ? 2 : 4];
+}
+
+void set_timing(bool on) {
+  std::lock_guard<std::mutex> g(g_timeline_lock);
+  g_timing = on;
+}
+
+// (name, milliseconds) of every launch timed since the last call, in launch
+// order; waits for the last of them.
+std::vector<std::tuple<std::string, double>> take_timeline() {
+  std::vector<std::tuple<std::string, hipEvent_t, hipEvent_t>> events;
+  {
+    std::lock_guard<std::mutex> g(g_timeline_lock);
+    events.swap(g_timeline);
+  }
+  std::vector<std::tuple<std::string, double>> out;
+  for (auto& [name, a, b] : events) {
+    float ms = 0.0f;
+    const bool ok = hipEventSynchronize(b) == hipSuccess &&
+                    hipEventElapsedTime(&ms, a, b) == hipSuccess;
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    TORCH_CHECK(ok, "nmce: reading a launch's HIP events failed");
+    out.emplace_back(name, ms);
+  }
+  return out;
+}
+
+}  // namespace
+
+PYBIND11_MODULE(_nmce_autograd, m) {
+  m.doc() = "The one-pass loss at TP = 1 as a C++ autograd node over libnmce's C ABI.";
+  m.def("one_pass_mean", &one_pass_mean, "mean one-pass loss (forward + backward in C++)");
+  m.def("assumed_of", &assumed_of, "the assumed upstream value saved by a one-pass loss");
+  m.def("set_timing", &set_timing, "time every launch with HIP events while on");
+  m.def("take_timeline", &take_timeline, "(name, ms) of the launches timed since the last call");
+}

@@ -1,10 +1,14 @@
-"""Compile ``libnmce.so`` (the gfx950 HIP kernels and their C ABI) in-tree.
+"""Compile ``libnmce.so`` (the gfx950 HIP kernels and their C ABI) and the
+``_nmce_autograd`` extension (the one-pass loss's autograd node, host C++ over
+that ABI) in-tree.
 
     python -m nmce._build          # from nano-megatron_amd/, or
     python -c "import __graft_entry__ as g; g.build()"   # from the repo root
 
-Every source is compiled to an object in parallel with ``hipcc`` for gfx950,
-then linked into ``nmce/libnmce.so``. No GPU is needed: hipcc cross-compiles.
+Every source is compiled to an object in parallel with ``hipcc`` (gfx950 for
+the kernels), then the kernels are linked into ``nmce/libnmce.so`` and the
+extension into ``nmce/_nmce_autograd<EXT_SUFFIX>`` against it and torch. No
+GPU is needed: hipcc cross-compiles.
 """
 
 from __future__ import annotations
@@ -14,6 +18,7 @@ import pathlib
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 PKG_DIR = pathlib.Path(__file__).resolve().parent
 PROJECT_DIR = PKG_DIR.parent  # nano-megatron_amd/
@@ -24,6 +29,9 @@ BUILD_DIR = PROJECT_DIR / "_build"
 LIB_PATH = PKG_DIR / "libnmce.so"
 
 SOURCES = ["nmce_ce.hip", "nmce_lmhead.hip"]
+EXT_SOURCE = "nmce_autograd.cpp"
+EXT_NAME = "_nmce_autograd"
+EXT_PATH = PKG_DIR / (EXT_NAME + sysconfig.get_config_var("EXT_SUFFIX"))
 
 ARCH = "gfx950"
 
@@ -62,8 +70,25 @@ def _noise(line: str) -> bool:
     return "packed-fp32-ops" in line and "not a recognized feature" in line
 
 
+def _ext_flags() -> tuple[list[str], list[str]]:
+    """Compile and link flags of the autograd extension: torch's and Python's
+    headers, torch's libraries, libnmce.so found next to the extension."""
+    from torch.utils import cpp_extension
+    import torch
+    abi = int(torch._C._GLIBCXX_USE_CXX11_ABI)
+    incs = [*cpp_extension.include_paths(), sysconfig.get_paths()["include"], str(INCLUDE_DIR)]
+    cflags = ["-O2", "-std=c++17", "-fPIC", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+              f"-DTORCH_EXTENSION_NAME={EXT_NAME}", "-DTORCH_API_INCLUDE_EXTENSION_H",
+              *[f"-I{p}" for p in incs]]
+    lflags = [*[f"-L{p}" for p in cpp_extension.library_paths()], f"-L{PKG_DIR}", "-lnmce",
+              "-lc10", "-lc10_hip", "-ltorch", "-ltorch_cpu", "-ltorch_python",
+              "-Wl,-rpath,$ORIGIN"]
+    return cflags, lflags
+
+
 def build(verbose: bool = False) -> pathlib.Path:
-    """Compile every source and link ``libnmce.so``; returns the library path."""
+    """Compile every source, link ``libnmce.so`` and the autograd extension;
+    returns the library path."""
     BUILD_DIR.mkdir(exist_ok=True)
     cc = hipcc()
     procs = []
@@ -73,6 +98,10 @@ def build(verbose: bool = False) -> pathlib.Path:
         objects.append(obj)
         cmd = [cc, *HIPCC_FLAGS, "-c", str(CSRC_DIR / src), "-o", str(obj)]
         procs.append((src, _run(cmd, verbose)))
+    ext_cflags, ext_lflags = _ext_flags()
+    ext_obj = BUILD_DIR / (pathlib.Path(EXT_SOURCE).stem + ".o")
+    procs.append((EXT_SOURCE, _run([cc, *ext_cflags, "-c", str(CSRC_DIR / EXT_SOURCE), "-o",
+                                    str(ext_obj)], verbose)))
     failed = []
     for src, proc in procs:
         out, _ = proc.communicate()
@@ -91,6 +120,13 @@ def build(verbose: bool = False) -> pathlib.Path:
         print(out, file=sys.stderr)
         raise RuntimeError("linking libnmce.so failed")
     os.replace(tmp, LIB_PATH)
+    tmp = EXT_PATH.with_name(EXT_PATH.name + ".tmp")
+    proc = _run([cc, "-shared", "-fPIC", "-o", str(tmp), str(ext_obj), *ext_lflags], verbose)
+    out, _ = proc.communicate()
+    if proc.returncode:
+        print(out, file=sys.stderr)
+        raise RuntimeError(f"linking {EXT_PATH.name} failed")
+    os.replace(tmp, EXT_PATH)
     return LIB_PATH
 
 

@@ -101,6 +101,26 @@ def load() -> ctypes.CDLL:
     return _lib
 
 
+_ext = None
+
+
+def autograd_ext():
+    """The ``_nmce_autograd`` extension (the one-pass loss's autograd node,
+    built beside ``libnmce.so`` and linked against it), imported once."""
+    global _ext
+    if _ext is None:
+        load()  # libnmce.so first, from this package's directory
+        try:
+            from . import _nmce_autograd
+        except ImportError as e:
+            raise NmceError(
+                f"the _nmce_autograd extension is not built next to {LIB_PATH} ({e}); run "
+                "`python -m nmce._build` in nano-megatron_amd/ (or __graft_entry__.build())"
+            ) from e
+        _ext = _nmce_autograd
+    return _ext
+
+
 def check(status: int, what: str) -> None:
     if status != 0:
         msg = load().nmce_status_string(status).decode()

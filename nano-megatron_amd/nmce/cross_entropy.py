@@ -31,7 +31,10 @@ Differences from the reference, all deliberate:
   logits (bit-identical to the two-pass path), and rescales an in-place one
   (within four fp32 or two bf16 units in the last place: the written
   gradient and the ratio are each rounded once; exact for a power-of-two
-  ratio). ``one_pass=False`` turns it off.
+  ratio). ``one_pass=False`` turns it off. This path's autograd node is C++
+  (``_nmce_autograd``, built beside ``libnmce.so``): a Python node's backward
+  costs the engine a hand-over to the interpreter, tens of microseconds per
+  call, which a small batch pays in full.
 * The gradient is written **in place** into the logits storage with
   ``inplace=True`` (as at model.py:277-281, where the logits come straight
   from the LM-head matmul, which does not save them): by the forward on the
@@ -415,93 +418,6 @@ def _one_pass_rows(logits: torch.Tensor, world_size: int) -> torch.Tensor | None
 _one_pass_limit: dict[int, int] = {}
 
 
-def _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint, inplace,
-                         bad_flag=None):
-    """Forward of the whole vocabulary that also writes the gradient of the mean
-    for the upstream value in ``hint`` (nmce_ce_fwd_bwd), from the same single
-    read of the logits: into the logits' own storage when ``inplace``, else
-    into a new buffer. Returns the flat per-token loss; the backward keeps that
-    gradient unless its upstream value differs. ``bad_flag``: the device count
-    of the target check enqueued just before; the kernel writes nothing when
-    it is nonzero. Only the wrapper calls it, after checking the inputs."""
-    lib = _lib.load()
-    dev = logits.device
-    n, V = rows.shape
-    ld = rows.stride(0) if n > 1 else V
-    tgt = target.reshape(-1)
-    if not tgt.is_contiguous():
-        tgt = tgt.contiguous()
-    out = torch.empty((3, n), dtype=torch.float32, device=dev)  # loss, max, exp-sum - 1
-    loss, row_stat = out[0], out[1:]
-    if inplace:
-        grad, ldg = rows, ld
-    else:
-        grad, ldg = torch.empty((n, V), dtype=rows.dtype, device=dev), V
-    assumed = torch.empty(1, dtype=torch.float32, device=dev)
-    _launch("nmce_ce_fwd_bwd", lib.nmce_ce_fwd_bwd, rows.data_ptr(), grad.data_ptr(),
-            _lib.dtype_code(rows.dtype), n, V, ld, ldg, tgt.data_ptr(), loss.data_ptr(),
-            row_stat[0].data_ptr(), row_stat[1].data_ptr(), hint.data_ptr(),
-            assumed.data_ptr(), _lib.ptr(bad_flag), float(n), _lib.stream_handle(dev))
-    ctx.vocab_start = vocab_start
-    ctx.logits_shape = logits.shape
-    ctx.ld = ld
-    ctx.inplace = inplace
-    ctx.hint = hint
-    ctx.handed_out = False
-    if inplace:
-        # The logits now hold the gradient: make autograd nodes that saved
-        # them fail their version check rather than read it.
-        torch.autograd.graph.increment_version(logits)
-        ctx.grad_buf = logits.detach()
-        ctx.save_for_backward(tgt, row_stat, assumed)
-    else:
-        ctx.save_for_backward(rows, tgt, row_stat, grad, assumed)
-    return loss
-
-
-def _ce_backward_one_pass(ctx, go, gdiv):
-    """Backward after ``_ce_forward_one_pass``. A separate buffer is left as it
-    is when ``go`` is the assumed upstream value and rewritten from the logits
-    otherwise, so the result equals the two-pass backward bit for bit. An
-    in-place one is rescaled instead (the logits are gone). Either way the
-    buffer is handed out once: a second backward through the same graph
-    (``retain_graph=True``) gets a new buffer from the logits, or raises when
-    they hold the gradient."""
-    lib = _lib.load()
-    stream = None
-    if ctx.inplace:
-        if ctx.handed_out:
-            raise RuntimeError(
-                "nmce: a second backward through an in-place one-pass loss needs the logits, "
-                "which now hold the gradient; pass inplace=False to differentiate it twice")
-        tgt, row_stat, assumed = ctx.saved_tensors
-        grad = ctx.grad_buf
-        n, V = tgt.numel(), ctx.logits_shape[-1]
-        stream = _lib.stream_handle(grad.device)
-        _launch("nmce_ce_grad_rescale_unless", lib.nmce_ce_grad_rescale_unless,
-                grad.data_ptr(), _lib.dtype_code(grad.dtype), n, V, ctx.ld, go.data_ptr(),
-                assumed.data_ptr(), ctx.hint.data_ptr(), stream)
-        ctx.handed_out = True
-        ctx.grad_buf = None
-        return grad
-    rows, tgt, row_stat, grad, assumed = ctx.saved_tensors
-    n, V = rows.shape
-    stream = _lib.stream_handle(rows.device)
-    if ctx.handed_out:
-        fresh = torch.empty((n, V), dtype=rows.dtype, device=rows.device)
-        _launch("nmce_ce_bwd_scaled", lib.nmce_ce_bwd_scaled,
-                rows.data_ptr(), fresh.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, V,
-                tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
-                go.data_ptr(), 0, gdiv, stream)
-        return fresh.view(ctx.logits_shape)
-    _launch("nmce_ce_bwd_scaled_unless", lib.nmce_ce_bwd_scaled_unless,
-            rows.data_ptr(), grad.data_ptr(), _lib.dtype_code(rows.dtype), n, V, ctx.ld, V,
-            tgt.data_ptr(), ctx.vocab_start, row_stat[0].data_ptr(), row_stat[1].data_ptr(),
-            go.data_ptr(), gdiv, assumed.data_ptr(), ctx.hint.data_ptr(), stream)
-    ctx.handed_out = True
-    return grad.view(ctx.logits_shape)
-
-
 def _grad_operand(grad_output):
     """(fp32 tensor, row stride) for the kernels; stride 0 for an expanded
     scalar such as the gradient torch's MeanBackward passes."""
@@ -564,27 +480,18 @@ class _VocabParallelCrossEntropy(torch.autograd.Function):
 
 class _VocabParallelCrossEntropyMean(torch.autograd.Function):
     """``_VocabParallelCrossEntropy`` followed by ``.mean()`` (cross_entropy.py:85)
-    as one node: the forward returns the 0-dim mean (torch's, on the same
-    per-token values), and the backward hands the scalar gradient of the mean
-    straight to the kernel, which divides it by the token count per row.
-    That is the same fp32 quotient torch's MeanBackward would expand, so the
-    gradient is bit-identical, without MeanBackward's two kernels.
+    as one node, on the two-pass path: the forward returns the 0-dim mean
+    (torch's, on the same per-token values), and the backward hands the scalar
+    gradient of the mean straight to the kernel, which divides it by the token
+    count per row. That is the same fp32 quotient torch's MeanBackward would
+    expand, so the gradient is bit-identical, without MeanBackward's two
+    kernels. (The one-pass path's node is ``_nmce_autograd.one_pass_mean``.)
     """
 
     @staticmethod
-    def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None,
-                hint=None, bad_flag=None):
-        # ``hint`` (the one-pass path's upstream value) is given only when a
-        # gradient is wanted; without it the forward writes no gradient.
-        rows = _one_pass_rows(logits, world_size) if hint is not None else None
-        ctx.one_pass = rows is not None
-        if ctx.one_pass:
-            loss = _ce_forward_one_pass(ctx, logits, rows, target, vocab_start, vocab_end, hint,
-                                        _resolve_inplace(logits, inplace, in_forward=True),
-                                        bad_flag)
-        else:
-            loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
-                               inplace)
+    def forward(ctx, logits, target, vocab_start, vocab_end, group, world_size, inplace=None):
+        loss = _ce_forward(ctx, logits, target, vocab_start, vocab_end, group, world_size,
+                           inplace)
         ctx.n_tokens = loss.numel()
         return loss.mean()
 
@@ -594,11 +501,25 @@ class _VocabParallelCrossEntropyMean(torch.autograd.Function):
         if go.dtype != torch.float32:
             go = go.float()
         gdiv = float(max(ctx.n_tokens, 1))
-        if ctx.one_pass:
-            grad = _ce_backward_one_pass(ctx, go, gdiv)
-        else:
-            grad = _ce_backward(ctx, go, 0, gdiv)
-        return grad, None, None, None, None, None, None, None, None
+        return _ce_backward(ctx, go, 0, gdiv), None, None, None, None, None, None
+
+
+def _one_pass_apply(logits, target, hint, bad_flag, inplace, vocab_start):
+    """The one-pass loss at TP = 1 (cross_entropy.py:16-65 and the mean of :85)
+    as a C++ autograd node over nmce_ce_fwd_bwd: one read of the logits writes
+    the per-token loss, the row statistics and the gradient of the mean for
+    the upstream value ``hint`` holds, into the logits' storage when
+    ``inplace`` or into a new buffer. Its backward keeps that gradient when its
+    upstream value is the assumed one; otherwise it rewrites a separate buffer
+    from the logits (bit-identical to the two-pass path) or rescales an
+    in-place one, writing the value it received into ``hint``. The buffer is
+    handed out once: a second backward through the same graph gets a new
+    buffer from the logits, or raises when they hold the gradient. ``target``
+    is flat and contiguous; ``bad_flag``, the target check's device word (the
+    kernel writes nothing when it is nonzero), or None. Returns the 0-dim
+    mean loss. Only the wrapper calls it, after checking the inputs."""
+    return _lib.autograd_ext().one_pass_mean(logits, target, hint, bad_flag, inplace,
+                                             vocab_start)
 
 
 def vocab_parallel_cross_entropy(
@@ -666,9 +587,16 @@ def vocab_parallel_cross_entropy(
     # the GPU is busy while the host reads the counts. They never read out of
     # bounds on a bad target; their result is discarded when the check fails.
     try:
-        loss = _VocabParallelCrossEntropyMean.apply(
-            logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace, hint,
-            bad_flag)
+        if hint is not None:
+            tgt = target.reshape(-1)
+            if not tgt.is_contiguous():
+                tgt = tgt.contiguous()
+            loss = _one_pass_apply(logits, tgt, hint, bad_flag,
+                                   _resolve_inplace(logits, inplace, in_forward=True),
+                                   vocab_start)
+        else:
+            loss = _VocabParallelCrossEntropyMean.apply(
+                logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace)
     except BaseException:
         if pending is not None:
             pending.wait()

@@ -418,6 +418,7 @@ def test_target_check_waits_when_the_loss_raises(monkeypatch):
     for one_pass in (True, False):
         x = torch.randn(2, 3, 16, device=DEV, requires_grad=True)
         monkeypatch.setattr(ce._VocabParallelCrossEntropyMean, "apply", boom)
+        monkeypatch.setattr(ce, "_one_pass_apply", boom)
         with pytest.raises(RuntimeError, match="planted"):
             nmce.vocab_parallel_cross_entropy(x * 1.0, t, 0, 16, ctx, one_pass=one_pass)
         monkeypatch.undo()
@@ -798,20 +799,25 @@ def test_one_pass_falls_back():
 
 
 class _HitRecorder:
-    """Wraps the one-pass backward and records (assumed, received) upstream
-    values: the forward's gradient stands when they are equal."""
+    """Records (assumed, received) upstream values of every one-pass loss's
+    backward: the value its forward assumed (saved by the autograd node) and
+    the gradient that reaches the loss (a hook, which runs before the node's
+    backward). The forward's gradient stands when they are equal."""
 
     def __init__(self, monkeypatch):
+        from nmce import _lib
         from nmce import cross_entropy as ce
         self.calls = []
-        original = ce._ce_backward_one_pass
+        original = ce._one_pass_apply
+        ext = _lib.autograd_ext()
 
-        def wrapped(ctx, go, gdiv):
-            assumed = ctx.saved_tensors[-1]
-            self.calls.append((assumed.item(), go.item()))
-            return original(ctx, go, gdiv)
+        def wrapped(*args):
+            loss = original(*args)
+            loss.register_hook(
+                lambda g: self.calls.append((ext.assumed_of(loss).item(), g.item())))
+            return loss
 
-        monkeypatch.setattr(ce, "_ce_backward_one_pass", wrapped)
+        monkeypatch.setattr(ce, "_one_pass_apply", wrapped)
 
 
 def test_one_pass_follows_the_upstream_value(monkeypatch):

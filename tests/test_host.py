@@ -32,6 +32,17 @@ def test_library_exports_every_declared_symbol(lib):
     assert set(L.SIGNATURES) == set(names), "ctypes signatures and header disagree"
 
 
+def test_autograd_extension_loads(lib):
+    """The one-pass loss's C++ autograd node is built next to libnmce.so, links
+    against it, and imports without a GPU; its timeline starts empty."""
+    from nmce import _lib as L
+    ext = L.autograd_ext()
+    assert pathlib.Path(ext.__file__).parent == L.LIB_PATH.parent
+    for name in ("one_pass_mean", "assumed_of", "set_timing", "take_timeline"):
+        assert hasattr(ext, name), name
+    assert ext.take_timeline() == []
+
+
 def test_status_strings(lib):
     assert lib.nmce_status_string(0) == b"ok"
     for code in range(-6, 0):
