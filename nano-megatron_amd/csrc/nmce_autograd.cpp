@@ -13,16 +13,20 @@
 // interpreter on its device thread for every backward, and the forward's
 // Python bookkeeping besides: tens of microseconds per call, which a small
 // batch (a step of a few tens of microseconds of kernels) pays in full. The
-// Python wrapper still validates the arguments, resolves the upstream hint
-// and runs the target check; this node does the rest.
+// Python wrapper still validates the arguments and resolves the upstream
+// hint; the target check of cross_entropy.py:79-81 runs here too
+// (one_pass_mean_checked).
 #include <torch/extension.h>
 #include <torch/csrc/autograd/variable.h>
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
+#include <chrono>
+#include <map>
 #include <mutex>
 #include <string>
 #include <tuple>
+#include <utility>
 #include <vector>
 
 #include "nmce.h"
@@ -185,6 +189,87 @@ struct OnePassMean : public torch::autograd::Function<OnePassMean> {
   }
 };
 
+// ---- the target check ------------------------------------------------------
+// nmce_validate_targets_once counts the targets outside [0, vocab) into a
+// pinned host word (for the ValueError) and a device word that the one-pass
+// kernel reads before its first store (it writes nothing when it is nonzero),
+// on the loss stream just before the kernel. The host waits for the check's
+// event after enqueueing the kernel, so the GPU starts on the loss meanwhile.
+
+// The device word per (device, stream): the check and the kernel run on that
+// stream one after the other, so calls on one stream can share it.
+std::mutex g_flag_lock;
+std::map<std::pair<int, hipStream_t>, at::Tensor> g_flags;
+
+at::Tensor flag_word(const at::Tensor& like, hipStream_t st) {
+  std::lock_guard<std::mutex> g(g_flag_lock);
+  auto key = std::make_pair(static_cast<int>(like.device().index()), st);
+  auto it = g_flags.find(key);
+  if (it == g_flags.end())
+    it = g_flags.emplace(key, at::empty({1}, like.options().dtype(at::kInt))).first;
+  return it->second;
+}
+
+// Pinned count words with their events, pooled and reused once a check has
+// been waited for (the kernel writes the word through its host mapping).
+struct CheckSlot {
+  at::Tensor host;
+  hipEvent_t event = nullptr;
+};
+std::mutex g_slot_lock;
+std::vector<CheckSlot> g_slots;
+
+CheckSlot take_slot() {
+  {
+    std::lock_guard<std::mutex> g(g_slot_lock);
+    if (!g_slots.empty()) {
+      CheckSlot s = g_slots.back();
+      g_slots.pop_back();
+      return s;
+    }
+  }
+  CheckSlot s;
+  s.host = at::empty({1}, at::TensorOptions().dtype(at::kInt).pinned_memory(true));
+  TORCH_CHECK(hipEventCreateWithFlags(&s.event, hipEventDisableTiming) == hipSuccess,
+              "nmce: hipEventCreateWithFlags failed");
+  return s;
+}
+
+// Waits for a recorded check on every way out of the call (the kernel writes
+// the pinned word until then), and gives the slot back.
+class CheckGuard {
+ public:
+  explicit CheckGuard(CheckSlot s) : slot_(std::move(s)) {}
+  int32_t* host() { return slot_.host.data_ptr<int32_t>(); }
+  hipEvent_t event() const { return slot_.event; }
+  void recorded() { recorded_ = true; }
+  // The count, once the check has finished. Polls first (the count is
+  // usually there within microseconds of the launch), then blocks.
+  int32_t wait() {
+    if (recorded_) {
+      pybind11::gil_scoped_release nogil;
+      const auto until = std::chrono::steady_clock::now() + std::chrono::microseconds(200);
+      hipError_t q = hipEventQuery(slot_.event);
+      while (q == hipErrorNotReady && std::chrono::steady_clock::now() < until)
+        q = hipEventQuery(slot_.event);
+      if (q == hipErrorNotReady) q = hipEventSynchronize(slot_.event);
+      recorded_ = false;
+      TORCH_CHECK(q == hipSuccess, "nmce: waiting for the target check failed: ",
+                  hipGetErrorString(q));
+    }
+    return *static_cast<volatile int32_t*>(slot_.host.data_ptr<int32_t>());
+  }
+  ~CheckGuard() {
+    if (recorded_) (void)hipEventSynchronize(slot_.event);
+    std::lock_guard<std::mutex> g(g_slot_lock);
+    g_slots.push_back(std::move(slot_));
+  }
+
+ private:
+  CheckSlot slot_;
+  bool recorded_ = false;
+};
+
 at::Tensor one_pass_mean(const at::Tensor& logits, const at::Tensor& target,
                          const at::Tensor& hint, const c10::optional<at::Tensor>& bad_flag,
                          bool inplace, int64_t vocab_start) {
@@ -192,6 +277,32 @@ at::Tensor one_pass_mean(const at::Tensor& logits, const at::Tensor& target,
                            ? reinterpret_cast<int64_t>(bad_flag->data_ptr<int32_t>())
                            : 0;
   return OnePassMean::apply(logits, target, hint, flag, inplace, vocab_start);
+}
+
+// one_pass_mean with the target check of cross_entropy.py:79-81 in front:
+// raises the reference's ValueError, after the kernel has left everything as
+// it was, when a target lies outside [0, vocab_total).
+at::Tensor one_pass_mean_checked(const at::Tensor& logits, const at::Tensor& target,
+                                 const at::Tensor& hint, int64_t vocab_total, bool inplace,
+                                 int64_t vocab_start) {
+  hipStream_t st = stream_of(logits);
+  const at::Tensor flag = flag_word(logits, st);
+  CheckGuard guard(take_slot());
+  check(nmce_validate_targets_once(target.data_ptr<int64_t>(), target.numel(), vocab_total,
+                                   guard.host(), flag.data_ptr<int32_t>(), st),
+        "nmce_validate_targets_once");
+  if (hipEventRecord(guard.event(), st) != hipSuccess) {
+    // The check may still write the slot's word: let it finish first.
+    (void)hipStreamSynchronize(st);
+    TORCH_CHECK(false, "nmce: hipEventRecord failed");
+  }
+  guard.recorded();
+  at::Tensor loss = OnePassMean::apply(logits, target, hint,
+                                       reinterpret_cast<int64_t>(flag.data_ptr<int32_t>()),
+                                       inplace, vocab_start);
+  if (guard.wait() != 0)
+    throw pybind11::value_error("target token id is outside the model vocabulary");
+  return loss;
 }
 
 // The assumed upstream value a one-pass loss's forward used, for tests that
@@ -236,6 +347,8 @@ std::vector<std::tuple<std::string, double>> take_timeline() {
 PYBIND11_MODULE(_nmce_autograd, m) {
   m.doc() = "The one-pass loss at TP = 1 as a C++ autograd node over libnmce's C ABI.";
   m.def("one_pass_mean", &one_pass_mean, "mean one-pass loss (forward + backward in C++)");
+  m.def("one_pass_mean_checked", &one_pass_mean_checked,
+        "one_pass_mean after the target check; ValueError on a target outside the vocabulary");
   m.def("assumed_of", &assumed_of, "the assumed upstream value saved by a one-pass loss");
   m.def("set_timing", &set_timing, "time every launch with HIP events while on");
   m.def("take_timeline", &take_timeline, "(name, ms) of the launches timed since the last call");

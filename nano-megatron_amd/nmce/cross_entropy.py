@@ -224,37 +224,16 @@ def _side_stream(device: torch.device) -> torch.cuda.Stream:
     return stream
 
 
-# Per (device, stream): the device word the one-workgroup target check writes
-# and the one-pass kernel reads. Both run on that stream, one after the
-# other, so calls on one stream can share it; calls on other streams have
-# their own.
-_flag_words: dict[tuple, torch.Tensor] = {}
-
-
-def _flag_word(device: torch.device, stream: int) -> torch.Tensor:
-    idx = device.index if device.index is not None else torch.cuda.current_device()
-    key = (idx, stream)
-    word = _flag_words.get(key)
-    if word is None:
-        word = torch.empty(1, dtype=torch.int32, device=device)
-        _flag_words[key] = word
-    return word
-
-
-def launch_target_check(target: torch.Tensor, vocab_size: int,
-                        on_side_stream: bool = True,
-                        device_flag: torch.Tensor | None = None) -> _PendingCheck | None:
+def launch_target_check(target: torch.Tensor, vocab_size: int) -> _PendingCheck | None:
     """Start the target check of cross_entropy.py:79-81 without blocking.
 
     One kernel counts targets outside ``[0, vocab_size)`` straight into pinned
     host memory, on a side stream ordered after the work already queued on the
     current stream; ``raise_if_bad()`` on the result waits for that kernel
     alone. The loss kernels go on the current stream meanwhile, so the check
-    adds nothing to the loss stream's timeline.
-
-    With ``device_flag`` (a one-element int32 device tensor) the check runs on
-    the current stream as one workgroup that also writes the count there, for
-    a loss kernel enqueued next that must write nothing on a bad target.
+    adds nothing to the loss stream's timeline. (The one-pass path runs its
+    check on the loss stream, with a device word its kernel reads, inside the
+    C++ call: ``_nmce_autograd.one_pass_mean_checked``.)
     """
     lib = _lib.load()
     t = target.reshape(-1)
@@ -263,29 +242,9 @@ def launch_target_check(target: torch.Tensor, vocab_size: int,
     n = t.numel()
     if n == 0:
         return None
-    slots = 1 if device_flag is not None else lib.nmce_validate_slots(n)
+    slots = lib.nmce_validate_slots(n)
     dev_index = t.device.index if t.device.index is not None else torch.cuda.current_device()
     host, event = _check_slot(dev_index, slots)
-    if device_flag is not None:
-        _launch("nmce_validate_targets", lib.nmce_validate_targets_once, t.data_ptr(), n,
-                vocab_size, host.data_ptr(), device_flag.data_ptr(),
-                _lib.stream_handle(t.device))
-        if dev_index == torch.cuda.current_device():
-            event.record()
-        else:
-            event.record(torch.cuda.current_stream(t.device))
-        return _PendingCheck(dev_index, host, event, slots)
-    if not on_side_stream:
-        # On the loss stream, ahead of a kernel that fills every compute unit
-        # for its whole run (the one-pass forward), so that the host's wait
-        # ends early instead of after that kernel.
-        _launch("nmce_validate_targets", lib.nmce_validate_targets, t.data_ptr(), n,
-                vocab_size, host.data_ptr(), _lib.stream_handle(t.device))
-        if dev_index == torch.cuda.current_device():
-            event.record()  # the current device's current stream
-        else:
-            event.record(torch.cuda.current_stream(t.device))
-        return _PendingCheck(dev_index, host, event, slots)
     main = torch.cuda.current_stream(t.device)
     side = _side_stream(t.device)
     side.wait_stream(main)  # the targets are complete in the current stream's order
@@ -504,7 +463,7 @@ class _VocabParallelCrossEntropyMean(torch.autograd.Function):
         return _ce_backward(ctx, go, 0, gdiv), None, None, None, None, None, None
 
 
-def _one_pass_apply(logits, target, hint, bad_flag, inplace, vocab_start):
+def _one_pass_apply(logits, target, hint, vocab_size, inplace, vocab_start):
     """The one-pass loss at TP = 1 (cross_entropy.py:16-65 and the mean of :85)
     as a C++ autograd node over nmce_ce_fwd_bwd: one read of the logits writes
     the per-token loss, the row statistics and the gradient of the mean for
@@ -515,11 +474,16 @@ def _one_pass_apply(logits, target, hint, bad_flag, inplace, vocab_start):
     in-place one, writing the value it received into ``hint``. The buffer is
     handed out once: a second backward through the same graph gets a new
     buffer from the logits, or raises when they hold the gradient. ``target``
-    is flat and contiguous; ``bad_flag``, the target check's device word (the
-    kernel writes nothing when it is nonzero), or None. Returns the 0-dim
-    mean loss. Only the wrapper calls it, after checking the inputs."""
-    return _lib.autograd_ext().one_pass_mean(logits, target, hint, bad_flag, inplace,
-                                             vocab_start)
+    is flat and contiguous. With ``vocab_size`` the target check of
+    cross_entropy.py:79-81 runs first on the same stream and leaves a device
+    word the kernel reads: on a target outside ``[0, vocab_size)`` the kernel
+    writes nothing and the reference's ``ValueError`` is raised once the
+    check's count is in; ``None`` skips the check. Returns the 0-dim mean
+    loss. Only the wrapper calls it, after checking the inputs."""
+    ext = _lib.autograd_ext()
+    if vocab_size is None:
+        return ext.one_pass_mean(logits, target, hint, None, inplace, vocab_start)
+    return ext.one_pass_mean_checked(logits, target, hint, vocab_size, inplace, vocab_start)
 
 
 def vocab_parallel_cross_entropy(
@@ -564,6 +528,8 @@ def vocab_parallel_cross_entropy(
     before this returns, and the logits are left as they were: on the
     one-pass path the check runs on the loss stream and the kernel writes
     nothing when it failed; the two-pass path writes only in its backward.
+    On the one-pass path the check, the kernel and the wait for the check's
+    count are one call into the C++ module (``_one_pass_apply``).
     """
     _check_inputs(logits, target, vocab_start, vocab_end)
     vocab_size = ctx.tp_size * (vocab_end - vocab_start)
@@ -576,27 +542,19 @@ def vocab_parallel_cross_entropy(
         else:
             _check_hint(upstream_hint, logits.device)
             hint = upstream_hint
-    bad_flag = None
-    if validate and hint is not None:
-        # the one-pass kernel reads the check's count before writing anything
-        bad_flag = _flag_word(logits.device, _lib.stream_handle(logits.device))
-    pending = (launch_target_check(target, vocab_size, on_side_stream=hint is None,
-                                   device_flag=bad_flag)
-               if validate else None)
+    if hint is not None:
+        tgt = target.reshape(-1)
+        if not tgt.is_contiguous():
+            tgt = tgt.contiguous()
+        return _one_pass_apply(logits, tgt, hint, vocab_size if validate else None,
+                               _resolve_inplace(logits, inplace, in_forward=True), vocab_start)
+    pending = launch_target_check(target, vocab_size) if validate else None
     # The loss kernels are enqueued before the host waits for the check, so
     # the GPU is busy while the host reads the counts. They never read out of
     # bounds on a bad target; their result is discarded when the check fails.
     try:
-        if hint is not None:
-            tgt = target.reshape(-1)
-            if not tgt.is_contiguous():
-                tgt = tgt.contiguous()
-            loss = _one_pass_apply(logits, tgt, hint, bad_flag,
-                                   _resolve_inplace(logits, inplace, in_forward=True),
-                                   vocab_start)
-        else:
-            loss = _VocabParallelCrossEntropyMean.apply(
-                logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace)
+        loss = _VocabParallelCrossEntropyMean.apply(
+            logits, target, vocab_start, vocab_end, ctx.tp_group, ctx.tp_size, inplace)
     except BaseException:
         if pending is not None:
             pending.wait()

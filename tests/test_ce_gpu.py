@@ -397,7 +397,10 @@ def test_out_of_vocabulary_target_raises():
 def test_target_check_waits_when_the_loss_raises(monkeypatch):
     """The check kernel writes its counts straight into a pinned host buffer,
     so a loss call that leaves on an exception must still wait for it before
-    the buffer can go back to the allocator; both wrappers do."""
+    the buffer can go back to the allocator; both wrappers do for the checks
+    they launch from Python (the two-pass and the fused path). The one-pass
+    path's check runs inside its C++ call, whose guard waits on every way out
+    (test_bad_target_leaves_in_place_logits_intact reuses its slots)."""
     import nmce
     from nmce import cross_entropy as ce
     from nmce import lmhead as lm
@@ -428,7 +431,7 @@ def test_target_check_waits_when_the_loss_raises(monkeypatch):
     monkeypatch.setattr(lm._LMHeadVocabParallelCrossEntropyMean, "apply", boom)
     with pytest.raises(RuntimeError, match="planted"):
         nmce.lmhead_vocab_parallel_cross_entropy(h, w, t.reshape(-1), 0, 16, ctx)
-    assert len(waited) == 3
+    assert len(waited) == 2
     assert all(p.event.query() for p in waited)
     # and the normal path still raises on a bad target after the direct write
     monkeypatch.undo()

@@ -38,7 +38,8 @@ def test_autograd_extension_loads(lib):
     from nmce import _lib as L
     ext = L.autograd_ext()
     assert pathlib.Path(ext.__file__).parent == L.LIB_PATH.parent
-    for name in ("one_pass_mean", "assumed_of", "set_timing", "take_timeline"):
+    for name in ("one_pass_mean", "one_pass_mean_checked", "assumed_of", "set_timing",
+                 "take_timeline"):
         assert hasattr(ext, name), name
     assert ext.take_timeline() == []
 
