@@ -21,6 +21,7 @@
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
+#include <atomic>
 #include <chrono>
 #include <map>
 #include <mutex>
@@ -45,6 +46,7 @@ int dtype_code(const at::Tensor& t) {
   if (t.scalar_type() == at::kFloat) return NMCE_F32;
   if (t.scalar_type() == at::kBFloat16) return NMCE_BF16;
   TORCH_CHECK(false, "nmce: unsupported logits dtype ", t.scalar_type());
+  return -1;
 }
 
 hipStream_t stream_of(const at::Tensor& t) {
@@ -55,7 +57,7 @@ hipStream_t stream_of(const at::Tensor& t) {
 // around every launch of this file while enabled, read back by
 // take_timeline() (the benchmark's per-call times).
 std::mutex g_timeline_lock;
-bool g_timing = false;
+std::atomic<bool> g_timing{false};
 std::vector<std::tuple<std::string, hipEvent_t, hipEvent_t>> g_timeline;
 
 template <typename Launch>
@@ -316,10 +318,7 @@ at::Tensor assumed_of(const at::Tensor& loss) {
   return saved[node->ctx_.saved_data.at("inplace").toBool() ? 2 : 4];
 }
 
-void set_timing(bool on) {
-  std::lock_guard<std::mutex> g(g_timeline_lock);
-  g_timing = on;
-}
+void set_timing(bool on) { g_timing = on; }
 
 // (name, milliseconds) of every launch timed since the last call, in launch
 // order; waits for the last of them.
