@@ -18,6 +18,7 @@
 // (one_pass_mean_checked).
 #include <torch/extension.h>
 #include <torch/csrc/autograd/variable.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <hip/hip_runtime_api.h>
 
@@ -67,11 +68,20 @@ void timed(const char* name, hipStream_t st, Launch&& launch) {
     return;
   }
   hipEvent_t a = nullptr, b = nullptr;
-  TORCH_CHECK(hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess,
-              "nmce: hipEventCreate failed");
-  TORCH_CHECK(hipEventRecord(a, st) == hipSuccess, "nmce: hipEventRecord failed");
+  const bool made = hipEventCreate(&a) == hipSuccess && hipEventCreate(&b) == hipSuccess;
+  if (!made || hipEventRecord(a, st) != hipSuccess) {
+    if (a) (void)hipEventDestroy(a);
+    if (b) (void)hipEventDestroy(b);
+    TORCH_CHECK(false, "nmce: creating or recording a timing event failed");
+  }
   const int status = launch();
-  TORCH_CHECK(hipEventRecord(b, st) == hipSuccess, "nmce: hipEventRecord failed");
+  if (hipEventRecord(b, st) != hipSuccess) {
+    (void)hipEventSynchronize(a);
+    (void)hipEventDestroy(a);
+    (void)hipEventDestroy(b);
+    check(status, name);
+    TORCH_CHECK(false, "nmce: recording a timing event failed");
+  }
   {
     std::lock_guard<std::mutex> g(g_timeline_lock);
     g_timeline.emplace_back(name, a, b);
@@ -89,6 +99,7 @@ struct OnePassMean : public torch::autograd::Function<OnePassMean> {
   static at::Tensor forward(AutogradContext* ctx, const at::Tensor& logits,
                             const at::Tensor& target, const at::Tensor& hint, int64_t bad_flag,
                             bool inplace, int64_t vocab_start) {
+    const c10::DeviceGuard device_guard(logits.device());
     const int64_t V = logits.size(-1);
     const at::Tensor rows = logits.view({-1, V});
     const int64_t n = rows.size(0);
@@ -127,6 +138,7 @@ struct OnePassMean : public torch::autograd::Function<OnePassMean> {
   }
 
   static variable_list backward(AutogradContext* ctx, variable_list grad_outputs) {
+    const c10::DeviceGuard device_guard(grad_outputs[0].device());
     at::Tensor go = grad_outputs[0].reshape({1});
     if (go.scalar_type() != at::kFloat) go = go.to(at::kFloat);
     go = go.contiguous();
@@ -287,6 +299,7 @@ at::Tensor one_pass_mean(const at::Tensor& logits, const at::Tensor& target,
 at::Tensor one_pass_mean_checked(const at::Tensor& logits, const at::Tensor& target,
                                  const at::Tensor& hint, int64_t vocab_total, bool inplace,
                                  int64_t vocab_start) {
+  const c10::DeviceGuard device_guard(logits.device());
   hipStream_t st = stream_of(logits);
   const at::Tensor flag = flag_word(logits, st);
   CheckGuard guard(take_slot());
@@ -329,15 +342,16 @@ std::vector<std::tuple<std::string, double>> take_timeline() {
     events.swap(g_timeline);
   }
   std::vector<std::tuple<std::string, double>> out;
+  bool ok = true;
   for (auto& [name, a, b] : events) {
     float ms = 0.0f;
-    const bool ok = hipEventSynchronize(b) == hipSuccess &&
-                    hipEventElapsedTime(&ms, a, b) == hipSuccess;
+    ok = ok && hipEventSynchronize(b) == hipSuccess &&
+         hipEventElapsedTime(&ms, a, b) == hipSuccess;
     (void)hipEventDestroy(a);
     (void)hipEventDestroy(b);
-    TORCH_CHECK(ok, "nmce: reading a launch's HIP events failed");
     out.emplace_back(name, ms);
   }
+  TORCH_CHECK(ok, "nmce: reading a launch's HIP events failed");
   return out;
 }
 
