@@ -1024,6 +1024,54 @@ def test_one_pass_default_leaves_logits_readable():
     assert torch.equal(grads[0].view(torch.int16), grads[1].view(torch.int16))
 
 
+def test_one_pass_on_a_side_stream():
+    """The validated one-pass path on a stream other than the default one: the
+    target check, its device word (one per device and stream) and the kernel
+    run on the caller's current stream, so the loss and the in-place gradient
+    are bit for bit those of the default stream; a bad target raises there
+    and leaves the logits intact, and the default stream's next call is
+    unaffected."""
+    import nmce
+    ctx = nmce.ParallelContext.single()
+    g = torch.Generator(device=DEV).manual_seed(23)
+    n, v = 512, 32000
+    x = torch.randn(n, v, device=DEV, generator=g).to(torch.bfloat16)
+    t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    hint = torch.ones(1, dtype=torch.float32, device=DEV)
+
+    def run(targets):
+        anchor = torch.zeros((), device=DEV, requires_grad=True)
+        logits = x.clone() + anchor.to(torch.bfloat16)
+        got = []
+        logits.register_hook(lambda gr: got.append(gr))
+        loss = nmce.vocab_parallel_cross_entropy(logits, targets, 0, v, ctx, inplace=True,
+                                                 upstream_hint=hint)
+        loss.backward()
+        return loss.detach(), got[0]
+
+    ref_loss, ref_grad = run(t)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        loss, grad = run(t)
+        bad = t.clone()
+        bad[n // 3] = v
+        anchor = torch.zeros((), device=DEV, requires_grad=True)
+        logits = x.clone() + anchor.to(torch.bfloat16)
+        with pytest.raises(ValueError, match="target token id is outside the model vocabulary"):
+            nmce.vocab_parallel_cross_entropy(logits, bad, 0, v, ctx, inplace=True,
+                                              upstream_hint=hint)
+        intact = torch.equal(logits.detach().view(torch.int16), x.view(torch.int16))
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert intact
+    assert torch.equal(loss, ref_loss)
+    assert torch.equal(grad.view(torch.int16), ref_grad.view(torch.int16))
+    again_loss, again_grad = run(t)
+    assert torch.equal(again_loss, ref_loss)
+    assert torch.equal(again_grad.view(torch.int16), ref_grad.view(torch.int16))
+
+
 @pytest.mark.parametrize("v", [50304, 128256])
 def test_bad_target_leaves_in_place_logits_intact(v):
     """A target outside the vocabulary on the in-place one-pass path (the
