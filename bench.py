@@ -742,7 +742,7 @@ def main() -> int:
         result, details["c2"] = run_unfused(args, "c2", args.steps, args.warmup)
         out = _headline(result, args.steps, args.warmup, WORKLOADS["c2"])
         for key, name, opts in NESTED:
-            print(f"[bench] {key}: {name} {opts}", file=sys.stderr, flush=True)
+            print(f"[bench] {key}", file=sys.stderr, flush=True)
             if WORKLOADS[name].get("fused"):
                 out[key], details[key] = run_fused(args, name, args.fused_steps,
                                                    args.fused_warmup, **opts)
@@ -765,10 +765,29 @@ def main() -> int:
             out["cpu_baseline"] = None
             for key, _, _ in NESTED:
                 out[key]["cpu_baseline"] = None
+        out["summary"] = _summary(out)
     if args.detail:
         pathlib.Path(args.detail).write_text(json.dumps(details, indent=1))
     print(json.dumps(_round(out), separators=(",", ":")), flush=True)
     return 0
+
+
+SUMMARY_COLS = ["tokens/s", "ms_per_step", "roofline.kernel", "roofline.frac",
+                "roofline.traffic", "cpu_baseline.value", "cpu_baseline.cores"]
+
+
+def _summary(out: dict) -> dict:
+    """One short row per configuration, last on the line, so that a reader
+    who keeps only the end of the output (about 2 KB) still sees every
+    configuration's throughput, roofline fraction and CPU baseline."""
+    def row(r: dict) -> list:
+        rf, cb = r["roofline"], r.get("cpu_baseline") or {}
+        return [r["value"], r["ms_per_step"], rf["kernel"].removeprefix("nmce_"),
+                rf["frac"], rf["traffic"], cb.get("value"), cb.get("cores")]
+    rows = {"cols": SUMMARY_COLS, "c2": row(out)}
+    for key, _, _ in NESTED:
+        rows[key] = row(out[key])
+    return rows
 
 
 def _headline(result: dict, steps: int, warmup: int, wl: dict) -> dict:

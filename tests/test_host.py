@@ -307,3 +307,37 @@ def test_bench_refuses_more_than_one_gpu():
                        capture_output=True, text=True, timeout=120)
     assert r.returncode == 2
     assert "exactly one GPU" in r.stdout
+
+
+def test_bench_summary_fits_the_end_of_the_line():
+    """The default line ends with one row per configuration; with realistic
+    figures the rows stay inside the last 1.5 KB of the line, so a reader that
+    keeps only the end of the output still sees every configuration."""
+    import importlib.util
+    import json
+    spec = importlib.util.spec_from_file_location("bench_under_test", ROOT / "bench.py")
+    bench = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(bench)
+
+    def result(kernel, frac):
+        return {"value": 12345678.9, "ms_per_step": 0.123456, "config": {"workload": "w"},
+                "roofline": {"bound": "hbm", "kernel": kernel, "achieved": 6000.1,
+                             "peak": 8000.0, "unit": "GB/s", "frac": frac,
+                             "traffic": 34219982819},
+                "step_frac": 0.7,
+                "cpu_baseline": {"value": 1234567.8, "unit": "tokens/s", "cores": 16,
+                                 "kind": "port", "sample": "s" * 80}}
+    out = {"metric": bench.METRIC, **result("nmce_ce_fwd_bwd", 0.759)}
+    for key, _, _ in bench.NESTED:
+        out[key] = result("nmce_lmhead_ce_fused_chunk_grads", 0.4633)
+    out["summary"] = bench._summary(out)
+    line = json.dumps(bench._round(out), separators=(",", ":"))
+    tail = line[line.index('"summary"'):]
+    assert len(tail) < 1500, len(tail)
+    back = json.loads(line)["summary"]
+    assert list(back) == ["cols", "c2"] + [k for k, _, _ in bench.NESTED]
+    for key in back:
+        if key != "cols":
+            row = dict(zip(back["cols"], back[key]))
+            assert row["roofline.frac"] in (0.759, 0.4633)
+            assert row["cpu_baseline.value"] == 1235000.0 and row["cpu_baseline.cores"] == 16
