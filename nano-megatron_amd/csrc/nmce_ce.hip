@@ -576,8 +576,7 @@ __global__ __launch_bounds__(kBlock, 2 * kBlock / 256) void ce_fwdbwd_kernel(
         for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
         out = E::pack(y);
       }
-      __builtin_amdgcn_raw_buffer_store_b128(out, rsrc_k(g, row, ldg, k), voff, 0,
-                                             kBufNonTemporal);
+      buffer_store_b128<kBufNonTemporal>(out, rsrc_k(g, row, ldg, k), voff);
     }
     // Every lane stores; only the owner's offset is inside the row.
     const bool mine = owned && (static_cast<int>(lt) / EPV) % kBlock == tid;
@@ -733,8 +732,7 @@ __global__ __launch_bounds__(kStatsBlock) void ce_fwdbwd_wide_kernel(
       E::unpack(v, f);
 #pragma unroll
       for (int e = 0; e < EPV; ++e) y[e] = exp_shift(f[e], M) * scale;
-      __builtin_amdgcn_raw_buffer_store_b128(E::pack(y), grs, voff, k * kBlock * 16,
-                                             kBufNonTemporal);
+      buffer_store_b128<kBufNonTemporal>(E::pack(y), grs, voff + k * kBlock * 16);
     };
     // The LDS part first, so that the next row's LDS part can stream in
     // while the register part's gradient is written.

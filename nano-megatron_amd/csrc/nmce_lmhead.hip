@@ -723,11 +723,12 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
 // kVec (N % 4 == 0, ldc % 4 == 0, Cf 16-byte and C 8-byte aligned, 512 rows
 // within 32-bit offsets): buffer resources on the wave's first row, the
 // lane's column in the one offset register and the row step in the scalar
-// offset. The hardware range check covers the per-lane offset only, so rows
-// past M (passes p >= np, uniform) are skipped explicitly, and a lane whose
-// columns lie past N gets the resource's size as its offset: its accesses
-// are out of range (no memory access, a load reads 0, a store is dropped)
-// whether or not the scalar offset takes part in the check. Every access
+// offset of the loads (the 16-byte stores take it in the per-lane offset:
+// buffer_store_b128). The hardware range check covers the per-lane offset
+// only, so rows past M (passes p >= np, uniform) are skipped explicitly, and
+// a lane whose columns lie past N gets the resource's size as its offset: its
+// accesses are out of range (no memory access, a load reads 0, a store is
+// dropped) whether or not the row step takes part in the check. Every access
 // left is inside the matrix. In modes 2 and 3 half of the 16 loads of Cf
 // are issued before the pass is staged, so their latency runs under the
 // staging, and the other half right after it. Cf is streamed (non-temporal)
@@ -822,7 +823,7 @@ __device__ __forceinline__ void store_f32_tile(const Acc& acc, char* lds, float*
         if (p >= np) continue;
         const uint32_t so = static_cast<uint32_t>(row_off(p) * ldc * 4);
         if constexpr (kMode == 1) {
-          __builtin_amdgcn_raw_buffer_store_b128(sv, rf, vf, so, kNt);
+          buffer_store_b128<kNt>(sv, rf, vf + so);
         } else {
           const u32x4 o = old[p];
           const float v0 = __uint_as_float(sv.x) + __uint_as_float(o.x);
@@ -830,10 +831,10 @@ __device__ __forceinline__ void store_f32_tile(const Acc& acc, char* lds, float*
           const float v2 = __uint_as_float(sv.z) + __uint_as_float(o.z);
           const float v3 = __uint_as_float(sv.w) + __uint_as_float(o.w);
           if constexpr (kMode == 2) {
-            __builtin_amdgcn_raw_buffer_store_b128(
+            buffer_store_b128<kNt>(
                 u32x4{__float_as_uint(v0), __float_as_uint(v1), __float_as_uint(v2),
                       __float_as_uint(v3)},
-                rf, vf, so, kNt);
+                rf, vf + so);
           } else {
             typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
             const auto rh = __builtin_amdgcn_make_buffer_rsrc(
@@ -847,6 +848,63 @@ __device__ __forceinline__ void store_f32_tile(const Acc& acc, char* lds, float*
       }
     }
     __syncthreads();  // the next pass reuses S
+  }
+}
+
+// bf16 out through the freed LDS, as lmhead_p_kernel stages P^T: words of two
+// rows (vp = row / 2) per column, columns XOR-swizzled by the row pair, then
+// 16-byte stores of 512-byte row segments. Tiles that reach past N, and
+// outputs that are not 16-byte aligned, store element by element.
+__device__ __forceinline__ void store_bf16_tile(const Acc& acc, char* lds,
+                                                uint16_t* __restrict__ C, int64_t ldc, int64_t M,
+                                                int64_t N, int64_t m0, int64_t n0) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int fhalf = lane >> 5;
+  const bool vec_ok = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0;
+  __syncthreads();  // every wave is done with the operand buffers
+  uint32_t* P = reinterpret_cast<uint32_t*>(lds);
+  auto pcol = [](int vp, int t) { return t ^ (((vp >> 2) & 15) << 2); };
+#pragma unroll
+  for (int fn = 0; fn < kFN; ++fn) {
+    const int cloc = wn * kWaveN + 32 * fn + (lane & 31);
+#pragma unroll
+    for (int fm = 0; fm < kFM; ++fm)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        uint32_t* w = stage_word(P + (wm * kWaveM / 2 + 2 * fhalf) * kBN, fm, q, cloc);
+        w[0] = pack_bf16x2(acc.c[fm][fn][4 * q], acc.c[fm][fn][4 * q + 1]);
+        w[kBN] = pack_bf16x2(acc.c[fm][fn][4 * q + 2], acc.c[fm][fn][4 * q + 3]);
+      }
+  }
+  __syncthreads();
+#pragma unroll 2
+  for (int it = 0; it < (kBM / 2) * (kBN / 8) / kThreads; ++it) {
+    const int lin = it * kThreads + static_cast<int>(threadIdx.x);
+    const int vp = lin / (kBN / 8);
+    const int c0 = 8 * (lin % (kBN / 8));
+    const u32x4 a = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, c0));
+    const u32x4 b = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, c0 + 4));
+    const u32x4 lo = {(a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
+                      (b.x & 0xffffu) | (b.y << 16), (b.z & 0xffffu) | (b.w << 16)};
+    const u32x4 hi = {(a.x >> 16) | (a.y & 0xffff0000u), (a.z >> 16) | (a.w & 0xffff0000u),
+                      (b.x >> 16) | (b.y & 0xffff0000u), (b.z >> 16) | (b.w & 0xffff0000u)};
+    const int64_t col0 = n0 + c0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int64_t row = m0 + 2 * vp + h;
+      if (row >= M || col0 >= N) continue;
+      const u32x4 w = h ? hi : lo;
+      uint16_t* dst = C + row * ldc + col0;
+      if (vec_ok && col0 + 8 <= N) {
+        *reinterpret_cast<u32x4*>(dst) = w;
+      } else {
+        const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
+        for (int e = 0; e < 8 && col0 + e < N; ++e)
+          dst[e] = static_cast<uint16_t>(e & 1 ? ws[e >> 1] >> 16 : ws[e >> 1] & 0xffffu);
+      }
+    }
   }
 }
 
@@ -888,65 +946,10 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
   Acc acc;
   gemm_mainloop<kAMN, kBMN>(As, lda, M, Bs, ldb, N, kl, m0, n0, lds, acc, ka_rows - k0,
                             kb_rows - k0);
-
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave / kWavesN, wn = wave % kWavesN;
-  const int fhalf = lane >> 5;
-  if constexpr (kMode != 0) {
+  if constexpr (kMode != 0)
     store_f32_tile<kMode, kVec>(acc, lds, Cf, C, ldc, M, N, m0, n0);
-    return;
-  } else {
-    // bf16 out through the freed LDS, as lmhead_p_kernel stages P^T: words
-    // of two rows (vp = row / 2) per column, columns XOR-swizzled by the row
-    // pair, then 16-byte stores of 512-byte row segments. Tiles that reach
-    // past N, and outputs that are not 16-byte aligned, store element by
-    // element.
-    const bool vec_ok = (ldc & 7) == 0 && (reinterpret_cast<uintptr_t>(C) & 15) == 0;
-    __syncthreads();  // every wave is done with the operand buffers
-    uint32_t* P = reinterpret_cast<uint32_t*>(lds);
-    auto pcol = [](int vp, int t) { return t ^ (((vp >> 2) & 15) << 2); };
-#pragma unroll
-    for (int fn = 0; fn < kFN; ++fn) {
-      const int cloc = wn * kWaveN + 32 * fn + (lane & 31);
-#pragma unroll
-      for (int fm = 0; fm < kFM; ++fm)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          uint32_t* w = stage_word(P + (wm * kWaveM / 2 + 2 * fhalf) * kBN, fm, q, cloc);
-          w[0] = pack_bf16x2(acc.c[fm][fn][4 * q], acc.c[fm][fn][4 * q + 1]);
-          w[kBN] = pack_bf16x2(acc.c[fm][fn][4 * q + 2], acc.c[fm][fn][4 * q + 3]);
-        }
-    }
-    __syncthreads();
-#pragma unroll 2
-    for (int it = 0; it < (kBM / 2) * (kBN / 8) / kThreads; ++it) {
-      const int lin = it * kThreads + static_cast<int>(threadIdx.x);
-      const int vp = lin / (kBN / 8);
-      const int c0 = 8 * (lin % (kBN / 8));
-      const u32x4 a = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, c0));
-      const u32x4 b = *reinterpret_cast<const u32x4*>(P + vp * kBN + pcol(vp, c0 + 4));
-      const u32x4 lo = {(a.x & 0xffffu) | (a.y << 16), (a.z & 0xffffu) | (a.w << 16),
-                        (b.x & 0xffffu) | (b.y << 16), (b.z & 0xffffu) | (b.w << 16)};
-      const u32x4 hi = {(a.x >> 16) | (a.y & 0xffff0000u), (a.z >> 16) | (a.w & 0xffff0000u),
-                        (b.x >> 16) | (b.y & 0xffff0000u), (b.z >> 16) | (b.w & 0xffff0000u)};
-      const int64_t col0 = n0 + c0;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const int64_t row = m0 + 2 * vp + h;
-        if (row >= M || col0 >= N) continue;
-        const u32x4 w = h ? hi : lo;
-        uint16_t* dst = C + row * ldc + col0;
-        if (vec_ok && col0 + 8 <= N) {
-          *reinterpret_cast<u32x4*>(dst) = w;
-        } else {
-          const uint32_t ws[4] = {w.x, w.y, w.z, w.w};
-          for (int e = 0; e < 8 && col0 + e < N; ++e)
-            dst[e] = static_cast<uint16_t>(e & 1 ? ws[e >> 1] >> 16 : ws[e >> 1] & 0xffffu);
-        }
-      }
-    }
-  }
+  else
+    store_bf16_tile(acc, lds, C, ldc, M, N, m0, n0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1427,6 +1430,7 @@ int device_cus() {
   }
   return n_cu;
 }
+
 
 // K ranges for a product of `tiles` output tiles over K (a multiple of kBK)
 // on `cus` compute units, one 256x256 tile per compute unit at a time: the

@@ -299,6 +299,22 @@ def test_product_never_imports_the_oracle():
                 assert not m.split(".")[0] == "oracle", f"{path.name} imports {m}"
 
 
+def test_wide_buffer_stores_go_through_the_helper():
+    """Buffer stores wider than 8 bytes are issued only by buffer_store_b128,
+    which keeps the scalar offset the constant 0: with a register scalar
+    offset the compiler omits the wait state a VALU write of the store's data
+    registers needs right after the store."""
+    import re
+    csrc = ROOT / "nano-megatron_amd" / "csrc"
+    pattern = re.compile(r"__builtin_amdgcn_raw_buffer_store_b(96|128)\b")
+    for path in sorted(csrc.glob("*.hip")) + sorted(csrc.glob("*.h")):
+        for i, line in enumerate(path.read_text().splitlines(), 1):
+            if pattern.search(line):
+                assert path.name == "nmce_device.h", f"{path.name}:{i}: {line.strip()}"
+    helper = (csrc / "nmce_device.h").read_text()
+    assert "__builtin_amdgcn_raw_buffer_store_b128(v, r, voff, 0, kAux)" in helper
+
+
 def test_bench_refuses_more_than_one_gpu():
     """bench.py runs on exactly one GPU: --gpus 2 exits with status 2 and says why."""
     import subprocess

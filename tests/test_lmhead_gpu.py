@@ -755,6 +755,74 @@ def test_one_pass_fused_against_oracle(n, h, v, chunk):
     check_grad(wd.grad.float().cpu().numpy(), rdw, "dW")
 
 
+@pytest.mark.parametrize("n,chunk", [(2048, 2048), (2000, 512)])
+def test_fused_dw_product_is_bit_identical(n, chunk):
+    """The one-pass path's dW product of each token chunk (V = 33000, 129
+    tile rows with a ragged last one, x H = 1024) equals the GEMM core's own
+    products on the same dZ^T, as the chunks leave it in the workspace: with
+    one chunk (bf16 out) nmce_gemm_mn_bf16's product; with four chunks, the
+    last one short (fp32 accumulation, rounded to bf16 by the last), the
+    core's fp32 products of the chunks (nmce_gemm_nt_bf16 on X_c^T, zero past
+    the chunk's tokens) summed in chunk order and rounded once. Compared as
+    values (the two may differ in the sign of a zero only). The fp32
+    read-add-store epilogue checked here is where a VALU write of a 16-byte
+    store's data registers right after the store corrupts the first dword of
+    some lanes, when the compiler omits the wait state (buffer_store_b128)."""
+    from nmce import _lib as L
+    from nmce import lmhead
+    lib = L.load()
+    h, v = 1024, 33000
+    print(f"[gpu] chunked dW product n={n} chunk={chunk} v={v} h={h}", flush=True)
+    x, w, t = make_inputs(n, h, v, seed=71, w_std=0.5)
+    xd, wd, td = x.to(DEV), w.to(DEV), t.to(DEV)
+    stream = L.stream_handle(torch.device(DEV))
+    lay = lmhead._fused_layout(lib, n, h, v, chunk)
+    ws = torch.zeros(lay["total"], dtype=torch.uint8, device=DEV)
+    args = (xd.data_ptr(), wd.data_ptr(), L.NMCE_BF16, n, h, v)
+    local = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    out = torch.empty((3, n), dtype=torch.float32, device=DEV)
+    go = torch.ones(1, dtype=torch.float32, device=DEV)
+    dx = torch.empty((n, h), dtype=torch.bfloat16, device=DEV)
+    dw = torch.empty((v, h), dtype=torch.bfloat16, device=DEV)
+    ldt, vpad, step = lay["ldt"], lay["vpad"], lay["chunk"]
+    pt = lay["off_pt"]
+    dzt = ws[pt:pt + vpad * ldt * 2].view(torch.bfloat16).view(vpad, ldt)  # dZ_c^T after grads
+    acc = ref = None
+    for c in range(lay["n_chunks"]):
+        t0 = c * step
+        nc = min(step, n - t0)
+        L.check(lib.nmce_lmhead_ce_fused_chunk_stats(
+            *args, td.data_ptr(), 0, chunk, c, local[0].data_ptr(), local[1].data_ptr(),
+            local[2].data_ptr(), ws.data_ptr(), ws.numel(), stream), "chunk stats")
+        base = local.data_ptr() + 4 * t0
+        L.check(lib.nmce_ce_combine(base, base + 4 * n, base + 8 * n, 1, 3 * n, nc,
+                                    out[0].data_ptr() + 4 * t0, out[1].data_ptr() + 4 * t0,
+                                    out[2].data_ptr() + 4 * t0, stream), "combine")
+        L.check(lib.nmce_lmhead_ce_fused_chunk_grads(
+            *args, td.data_ptr(), 0, chunk, c, out[1].data_ptr(), out[2].data_ptr(),
+            local[2].data_ptr(), go.data_ptr(), 0, float(n), dx.data_ptr(), dw.data_ptr(),
+            ws.data_ptr(), ws.numel(), stream), "chunk grads")
+        if lay["n_chunks"] == 1:
+            assert ldt == n
+            ref = torch.empty((v, h), dtype=torch.bfloat16, device=DEV)
+            L.check(lib.nmce_gemm_mn_bf16(0, dzt.data_ptr(), ldt, xd.data_ptr(), h, v, h, ldt,
+                                          ref.data_ptr(), h, stream), "gemm_mn")
+        else:
+            xt = torch.zeros((h, ldt), dtype=torch.bfloat16, device=DEV)
+            xt[:, :nc] = xd[t0:t0 + nc].t()
+            part = torch.empty((v, h), dtype=torch.float32, device=DEV)
+            L.check(lib.nmce_gemm_nt_bf16(dzt.data_ptr(), ldt, xt.data_ptr(), ldt, v, h, ldt,
+                                          part.data_ptr(), L.NMCE_F32, h, stream), "gemm_nt")
+            acc = part if acc is None else acc + part
+    torch.cuda.synchronize()
+    if ref is None:
+        ref = acc.to(torch.bfloat16)
+    same = dw.float() == ref.float()
+    assert same.all(), (f"{int((~same).sum())} of {same.numel()} dW elements differ; first at "
+                        f"{torch.nonzero(~same)[0].tolist()}")
+    assert dw.float().abs().sum().item() > 0
+
+
 def test_one_pass_fused_follows_the_upstream_value():
     """A loss scaled by 0.25 each step: the first backward rescales the forward's
     gradients (a power-of-two ratio, so exactly) and records 0.25, after which
