@@ -221,17 +221,15 @@ def lm_head_stand_in():
     forward hands the resident logits on as a non-leaf tensor, backward
     receives d(logits) and stops there (the dX/dW GEMMs that would consume it
     are not part of the loss path). Without it the logits would be a leaf and
-    autograd would copy the whole gradient into ``.grad`` each step."""
-    import torch
+    autograd would copy the whole gradient into ``.grad`` each step. The node
+    is C++ (``head_output`` of the autograd extension), as the matmul's own
+    backward is, so the engine does not hand each backward to the
+    interpreter for it."""
+    from nmce import _lib as L
+    ext = L.autograd_ext()
 
-    class LMHeadOutput(torch.autograd.Function):
-        @staticmethod
-        def forward(ctx, logits, anchor):
-            return logits.view_as(logits)
-
-        @staticmethod
-        def backward(ctx, dlogits):
-            return None, None
+    class LMHeadOutput:
+        apply = staticmethod(ext.head_output)
 
     return LMHeadOutput
 

@@ -355,6 +355,29 @@ std::vector<std::tuple<std::string, double>> take_timeline() {
   return out;
 }
 
+// For measurements (no counterpart in the reference): an autograd node that
+// stands where the LM-head matmul is (model.py:192). Its forward hands the
+// resident logits on as a non-leaf alias, its backward receives d(logits)
+// and hands nothing further, as a C++ node, as the matmul's own backward
+// is, so a timed step carries no Python node of its own.
+struct HeadOutput : public torch::autograd::Function<HeadOutput> {
+  static at::Tensor forward(AutogradContext* ctx, const at::Tensor& logits,
+                            const at::Tensor& anchor) {
+    (void)ctx;
+    (void)anchor;
+    return logits.alias();
+  }
+  static variable_list backward(AutogradContext* ctx, variable_list grads) {
+    (void)ctx;
+    (void)grads;
+    return {at::Tensor(), at::Tensor()};
+  }
+};
+
+at::Tensor head_output(const at::Tensor& logits, const at::Tensor& anchor) {
+  return HeadOutput::apply(logits, anchor);
+}
+
 }  // namespace
 
 PYBIND11_MODULE(_nmce_autograd, m) {
@@ -365,4 +388,7 @@ PYBIND11_MODULE(_nmce_autograd, m) {
   m.def("assumed_of", &assumed_of, "the assumed upstream value saved by a one-pass loss");
   m.def("set_timing", &set_timing, "time every launch with HIP events while on");
   m.def("take_timeline", &take_timeline, "(name, ms) of the launches timed since the last call");
+  m.def("head_output", &head_output,
+        "logits as a non-leaf alias through a C++ node whose backward hands nothing on "
+        "(stands for the LM-head matmul in measurements)");
 }

@@ -39,9 +39,24 @@ def test_autograd_extension_loads(lib):
     ext = L.autograd_ext()
     assert pathlib.Path(ext.__file__).parent == L.LIB_PATH.parent
     for name in ("one_pass_mean", "one_pass_mean_checked", "assumed_of", "set_timing",
-                 "take_timeline"):
+                 "take_timeline", "head_output"):
         assert hasattr(ext, name), name
     assert ext.take_timeline() == []
+
+
+def test_head_output_node():
+    """The measurements' stand-in for the LM-head node: the logits come back as
+    a non-leaf alias (same storage) with a C++ grad_fn, and its backward hands
+    no gradient to the anchor. Pure autograd: it runs on CPU tensors."""
+    from nmce import _lib as L
+    ext = L.autograd_ext()
+    x = torch.randn(4, 6)
+    anchor = torch.zeros((), requires_grad=True)
+    y = ext.head_output(x, anchor)
+    assert y.requires_grad and not y.is_leaf and y.data_ptr() == x.data_ptr()
+    assert y.grad_fn is not None and "CppNode" in y.grad_fn.name()
+    (y * 2.0).sum().backward()
+    assert anchor.grad is None
 
 
 def test_status_strings(lib):
