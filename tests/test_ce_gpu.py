@@ -1162,6 +1162,42 @@ def test_one_pass_wide_rows(dtype, v):
         assert_close_rel(got, og, 1e-5, 1e-30, what="wide grad rows")
 
 
+@pytest.mark.parametrize("dtype,v", [(torch.bfloat16, 131080), (torch.float32, 65540)])
+def test_past_the_one_pass_width(dtype, v):
+    """One vector past the one-pass kernel's widest row the wrapper takes the
+    two-pass path (a Python autograd node, not the C++ one-pass node) and
+    still gives the reference's loss and gradient: the loss against an fp64
+    reference, sampled gradient rows against the oracle."""
+    import nmce
+    assert v > nmce._lib.load().nmce_ce_fwd_bwd_max_vocab(nmce._lib.dtype_code(dtype))
+    print(f"[gpu] past the one-pass width {dtype} V={v}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(23)
+    n = 300
+    x = (torch.randn(n, v, device=DEV, generator=g) * 2.0).to(dtype)
+    t = torch.randint(0, v, (n,), device=DEV, generator=g)
+    ctx = nmce.ParallelContext.single()
+    leaf = x.clone().requires_grad_(True)
+    loss = nmce.vocab_parallel_cross_entropy(leaf, t, 0, v, ctx)
+    assert "CppNode" not in loss.grad_fn.name(), loss.grad_fn.name()
+    loss.backward()
+    ref_loss = _torch_ref_rows(x, t)
+    assert abs(loss.item() - ref_loss.mean().item()) <= 1e-5 * abs(ref_loss.mean().item())
+    pick = torch.arange(0, n, 37, device=DEV)
+    _, og = ce_oracle.closed_form(x[pick].float().cpu().numpy(), t[pick].cpu().numpy(),
+                                  1.0 / n)
+    got = leaf.grad[pick].double().cpu().numpy()
+    if dtype == torch.bfloat16:
+        assert_bf16_close(got, og, what="grad rows past the one-pass width", atol=1e-30)
+    else:
+        assert_close_rel(got, og, 1e-5, 1e-30, what="grad rows past the one-pass width")
+    # one vector narrower takes the one-pass node
+    w = v - (8 if dtype == torch.bfloat16 else 4)
+    leaf2 = x[:, :w].contiguous().requires_grad_(True)
+    t2 = torch.remainder(t, w)
+    loss2 = nmce.vocab_parallel_cross_entropy(leaf2, t2, 0, w, ctx)
+    assert "CppNode" in loss2.grad_fn.name(), loss2.grad_fn.name()
+
+
 def test_one_pass_wide_extreme_rows():
     """The wide one-pass kernel against the two-pass path, bit for bit, on
     edge rows at V = 128256: -inf entries (30% of each row, never the

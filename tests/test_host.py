@@ -314,6 +314,29 @@ def test_product_never_imports_the_oracle():
                 assert not m.split(".")[0] == "oracle", f"{path.name} imports {m}"
 
 
+def test_one_pass_route_edges(lib):
+    """Which rows the wrapper hands to the one-pass kernel: TP = 1, fp32 or
+    bf16, a width of whole 16-byte vectors up to the kernel's limit (131072
+    bf16, 65536 fp32 columns), 16-byte aligned rows. One vector past the
+    limit, a ragged width, an unaligned row stride, TP > 1, fp16 and an empty
+    batch take the two-pass path. Host-side only (CPU tensors)."""
+    from nmce import cross_entropy as ce
+    from nmce import _lib as L
+    assert lib.nmce_ce_fwd_bwd_max_vocab(L.NMCE_BF16) == 131072
+    assert lib.nmce_ce_fwd_bwd_max_vocab(L.NMCE_F32) == 65536
+    take = ce._one_pass_rows
+    assert take(torch.zeros(2, 131072, dtype=torch.bfloat16), 1) is not None
+    assert take(torch.zeros(2, 131080, dtype=torch.bfloat16), 1) is None
+    assert take(torch.zeros(2, 65536), 1) is not None
+    assert take(torch.zeros(2, 65540), 1) is None
+    assert take(torch.zeros(3, 4, 1000, dtype=torch.bfloat16), 1) is not None
+    assert take(torch.zeros(2, 1001, dtype=torch.bfloat16), 1) is None  # not whole vectors
+    assert take(torch.zeros(2, 1009, dtype=torch.bfloat16)[:, :1008], 1) is None  # row stride
+    assert take(torch.zeros(2, 1000, dtype=torch.bfloat16), 2) is None  # TP > 1
+    assert take(torch.zeros(2, 1000, dtype=torch.float16), 1) is None
+    assert take(torch.zeros(0, 1000, dtype=torch.bfloat16), 1) is None
+
+
 def test_wide_buffer_stores_go_through_the_helper():
     """Buffer stores wider than 8 bytes are issued only by buffer_store_b128,
     which keeps the scalar offset the constant 0: with a register scalar
