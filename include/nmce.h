@@ -370,11 +370,11 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
  * P = exp(z - block max) in the workspace; once the chunk's statistics are
  * combined across the TP group, dZ follows from P by one factor per
  * (128-row block, token), in place, and the dX rows of the chunk and its
- * share of dW are formed by libnmce's GEMM, which reads dZ^T, the weight and
- * the hidden rows as they lie (no transposed copies). The one buffer that
- * grows with both sizes is a chunk's P, then dZ^T: bf16 [vocab_local,
- * token_chunk], the size of the bf16 logits when the chunk holds every
- * token. The logits are computed once: 6 * n_rows * vocab_local *
+ * share of dW are formed by libnmce's GEMM, which reads dZ^T and the weight
+ * as they lie and the chunk's hidden rows transposed (hidden_size x
+ * token_chunk bf16). The one buffer that grows with both sizes is a chunk's
+ * P, then dZ^T: bf16 [vocab_local, token_chunk], the size of the bf16 logits
+ * when the chunk holds every token. The logits are computed once: 6 * n_rows * vocab_local *
  * hidden_size flops in all.
  * Replaces model.py:192 followed by cross_entropy.py:17-65 and the matmul
  * backward of model.py:192; with a caller that assumes the right upstream
@@ -383,18 +383,20 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
  * --------------------------------------------------------------------------- */
 
 /*
- * Workspace layout (int64 values) written to layout[0 .. 10]:
+ * Workspace layout (int64 values) written to layout[0 .. 11]:
  *   [0] total bytes  [1] chunk (tokens per chunk)  [2] n_chunks
  *   [3] ldt (chunk padded to 64)  [4] vpad (vocab_local padded to 256)
  *   [5] nb (ceil(vocab_local / 128))  [6..9] byte offsets of P^T
- *   (= dZ_c^T, [vpad, ldt]: the only chunk-sized buffer; both backward
- *   products read it, hidden and weight as they lie), the partial statistics,
+ *   (= dZ_c^T, [vpad, ldt]: the only buffer that grows with the vocabulary
+ *   and the chunk; both backward products read it), the partial statistics,
  *   the fp32 dW accumulator (present when n_chunks > 1) and the fp32 partials
  *   of a chunk's dX product when it is split over K  [10] the number of K
  *   ranges of that product (1: not split; more when a chunk's dX has too few
- *   256x256 tiles to fill the current device's compute units).
+ *   256x256 tiles to fill the current device's compute units)  [11] byte
+ *   offset of the chunk's hidden rows transposed, X_c^T [hidden_size, ldt]
+ *   bf16 (the dW product's second operand), which runs to the end.
  */
-#define NMCE_LMHEAD_FUSED_LAYOUT_FIELDS 11
+#define NMCE_LMHEAD_FUSED_LAYOUT_FIELDS 12
 int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t vocab_local,
                                 int64_t token_chunk, int64_t* layout);
 

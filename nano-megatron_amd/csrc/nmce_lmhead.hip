@@ -28,11 +28,13 @@
 //             dX   = dZ W            (K = vocab; dZ^T and W both read
 //                                     vocabulary-row major, as they lie; split
 //                                     over K when the chunk's tiles are few)
-//             dW  += dZ^T X          (K = the chunk's tokens; X read token-row
-//                                     major, as it lies; fp32 across chunks
-//                                     only when there are several)
+//             dW  += dZ^T X          (K = the chunk's tokens; both operands
+//                                     K-contiguous: X_c^T, the chunk's hidden
+//                                     rows transposed, H x chunk bf16, tens of
+//                                     MB; fp32 across chunks only when there
+//                                     are several)
 // so 6 N V H flops in all, against 8 N V H for the recomputing backward, and
-// no transposed copy of any operand.
+// no copy of anything the size of the logits or the weight.
 //
 // Tokens are the MFMA N dimension in the loss GEMMs: the 32x32 accumulator
 // gives each lane 16 vocabulary rows of a single token, so the per-token
@@ -1471,6 +1473,7 @@ struct FusedLayout {
   int64_t dx_splits;  // K ranges of a chunk's dX product (split K when its tiles are few)
   int64_t dx_ks;      // their length
   int64_t off_dxp;    // their fp32 partials [dx_splits][chunk][h] (dx_splits > 1)
+  int64_t off_xt;     // the chunk's hidden rows transposed, X_c^T [h, ldt] bf16
 };
 
 FusedLayout fused_layout(int64_t n, int64_t h, int64_t v, int64_t token_chunk) {
@@ -1488,6 +1491,7 @@ FusedLayout fused_layout(int64_t n, int64_t h, int64_t v, int64_t token_chunk) {
   L.off_part = off; off += align256(3 * L.nb * L.chunk * 4);
   L.off_acc = off; off += L.n_chunks > 1 ? align256(v * h * 4) : 0;
   L.off_dxp = off; off += L.dx_splits > 1 ? align256(L.dx_splits * L.chunk * h * 4) : 0;
+  L.off_xt = off; off += align256(h * L.ldt * 2);
   L.total = off;
   return L;
 }
@@ -1810,8 +1814,8 @@ int nmce_lmhead_ce_fused_layout(int64_t n_rows, int64_t hidden_size, int64_t voc
   if (n_rows < 1 || hidden_size < 1 || vocab_local < 1) return NMCE_EINVAL_SHAPE;
   const FusedLayout L = fused_layout(n_rows, hidden_size, vocab_local, token_chunk);
   const int64_t v[NMCE_LMHEAD_FUSED_LAYOUT_FIELDS] = {
-      L.total,  L.chunk,    L.n_chunks, L.ldt,    L.vpad,     L.nb,
-      L.off_pt, L.off_part, L.off_acc,  L.off_dxp, L.dx_splits};
+      L.total,  L.chunk,    L.n_chunks, L.ldt,     L.vpad,      L.nb,
+      L.off_pt, L.off_part, L.off_acc,  L.off_dxp, L.dx_splits, L.off_xt};
   for (int i = 0; i < NMCE_LMHEAD_FUSED_LAYOUT_FIELDS; ++i) layout[i] = v[i];
   return NMCE_OK;
 }
@@ -1914,18 +1918,22 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
     if ((st = launch_status())) return st;
   }
   // dW (+)= dZ_c^T X_c: A = dZ^T (K = the chunk's padded tokens contiguous),
-  // B = the chunk's rows of X as they lie, token-major (zero dZ^T columns past
-  // the chunk, so X's k-rows stop at nc). Accumulated in fp32 across chunks
-  // and rounded to bf16 by the last.
+  // B = X_c^T [H, ldt], the chunk's hidden rows transposed first (zero past
+  // the chunk's tokens), so that both operands are K-contiguous: measured
+  // 0.14 ms faster per chunk of 4096 tokens at H = 4096 than reading X as it
+  // lies (MN-contiguous), for a transpose of 32 MB. The same products, bit
+  // for bit. Accumulated in fp32 across chunks and rounded to bf16 by the
+  // last.
   int mode;
   if (L.n_chunks == 1) mode = 0;
   else if (chunk_index == 0) mode = 1;
   else if (chunk_index + 1 < L.n_chunks) mode = 2;
   else mode = 3;
-  return launch_gemm_store(mode, pt, L.ldt, V, X + t0 * H, H, H, L.ldt,
+  auto* xt = reinterpret_cast<uint16_t*>(ws + L.off_xt);
+  if ((st = launch_transpose(X + t0 * H, nc, H, H, xt, L.ldt, s))) return st;
+  return launch_gemm_store(mode, pt, L.ldt, V, xt, L.ldt, H, L.ldt,
                            static_cast<uint16_t*>(grad_weight),
-                           reinterpret_cast<float*>(ws + L.off_acc), H, s, kGroupMProducts, false,
-                           true, 0, nc);
+                           reinterpret_cast<float*>(ws + L.off_acc), H, s, kGroupMProducts);
 }
 
 }  // extern "C"

@@ -70,7 +70,7 @@ SIGNATURES: dict[str, tuple] = {
 }
 
 NMCE_LMHEAD_LAYOUT_FIELDS = 10
-NMCE_LMHEAD_FUSED_LAYOUT_FIELDS = 11
+NMCE_LMHEAD_FUSED_LAYOUT_FIELDS = 12
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None

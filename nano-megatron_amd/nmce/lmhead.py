@@ -109,7 +109,7 @@ def _fused_layout(lib, n: int, hp: int, v: int, token_chunk: int) -> dict:
     _lib.check(lib.nmce_lmhead_ce_fused_layout(n, hp, v, token_chunk, ctypes.addressof(buf)),
                "nmce_lmhead_ce_fused_layout")
     keys = ("total", "chunk", "n_chunks", "ldt", "vpad", "nb", "off_pt", "off_part", "off_acc",
-            "off_dxp", "dx_splits")
+            "off_dxp", "dx_splits", "off_xt")
     return dict(zip(keys, (int(b) for b in buf)))
 
 

@@ -170,8 +170,11 @@ def test_default_chunk_never_holds_full_logits(lib):
         pt_bytes = off_part - off_pt
         assert pt_bytes == ((v + 255) // 256 * 256) * 4096 * 2
         assert 4 * pt_bytes <= logits_bytes + 4 * 256 * 4096 * 2
-        regions = [off_part - off_pt, off_acc - off_part, off_dxp - off_acc, total - off_dxp]
+        off_xt = buf[11]
+        regions = [off_part - off_pt, off_acc - off_part, off_dxp - off_acc,
+                   off_xt - off_dxp, total - off_xt]
         assert max(regions) == off_dxp - off_acc and max(regions) <= logits_bytes / 2
+        assert total - off_xt == h * 4096 * 2  # X_c^T, the dW product's second operand
         assert total < logits_bytes
         assert off_dxp - off_acc == (v * h * 4 + 255) // 256 * 256  # fp32 dW accumulator
     buf = (ctypes.c_int64 * 10)()
@@ -204,16 +207,18 @@ def test_one_pass_token_chunk_budget(lib):
     assert chunk(100000, 1 << 40) == 256  # at least one tile column
     buf = (ctypes.c_int64 * L.NMCE_LMHEAD_FUSED_LAYOUT_FIELDS)()
     # fields: total, chunk, n_chunks, ldt, vpad, nb, off_pt, off_part, off_acc, off_dxp,
-    # dx_splits
+    # dx_splits, off_xt
     assert lib.nmce_lmhead_ce_fused_layout(16384, 4096, 128256, 16384,
                                            ctypes.addressof(buf)) == 0
-    assert (buf[1], buf[2]) == (16384, 1) and buf[8] == buf[9] == buf[0]  # no accumulator
-    # P^T [vpad, ldt] bf16 is the only chunk-sized buffer: no transposed copies
+    assert (buf[1], buf[2]) == (16384, 1) and buf[8] == buf[9] == buf[11]  # no accumulator
+    # P^T [vpad, ldt] bf16 is the one buffer of the vocabulary's and the chunk's
+    # size; the chunk's hidden rows transposed, X_c^T [h, ldt], the only copy
     assert buf[7] - buf[6] == 128256 * 16384 * 2
+    assert buf[0] - buf[11] == 4096 * 16384 * 2
     n, v = 65536, 256000
     assert lib.nmce_lmhead_ce_fused_layout(n, 3072, v, chunk(n, v), ctypes.addressof(buf)) == 0
     assert buf[2] > 1 and buf[9] - buf[8] >= v * 3072 * 4  # fp32 dW accumulator
-    regions = [buf[6], buf[7], buf[8], buf[9], buf[0]]
+    regions = [buf[6], buf[7], buf[8], buf[9], buf[11], buf[0]]
     assert all(r % 256 == 0 for r in regions) and regions == sorted(regions)
 
 
@@ -233,7 +238,7 @@ def test_fused_dx_split_choice(lib):
         assert lib.nmce_lmhead_ce_fused_layout(n, h, v, ch, ctypes.addressof(buf)) == 0
         assert buf[10] == splits, (n, h, v, ch, buf[10])
         want = (splits * ch * h * 4 + 255) // 256 * 256 if splits > 1 else 0
-        assert buf[0] - buf[9] == want
+        assert buf[11] - buf[9] == want
 
 
 def test_validate_slots(lib):

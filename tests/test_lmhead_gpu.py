@@ -203,7 +203,7 @@ def test_gemm_nt(m, n, k, out):
 @pytest.mark.parametrize("a_mn", [1, 0])
 def test_gemm_mn_is_the_nt_product_of_the_transposes(m, n, k, a_mn):
     """The MN-contiguous operand path (ds_read_b64_tr_b16 fragments, used by
-    the fused backward products on dZ^T, W and X as they lie) gives the same
+    the fused dX product on dZ^T and W as they lie) gives the same
     bits as the K-contiguous one on the transposed operands: every lane's
     fragment holds the same 8 values in the same k order. Columns past m and
     n (up to the 8-element padding) hold NaN, which the product must not
