@@ -32,24 +32,15 @@
 namespace nmce {
 namespace {
 
-// Launch shapes (overridable at build time for sweeps; the fold order of the
-// statistics kernel, and so its bits, depends on NMCE_STATS_UNROLL, the flat
-// backward's results do not depend on its shape).
-#ifndef NMCE_STATS_UNROLL
-#define NMCE_STATS_UNROLL 2
-#endif
-#ifndef NMCE_FLAT_BLOCK
-#define NMCE_FLAT_BLOCK 128
-#endif
-#ifndef NMCE_FLAT_UNROLL
-#define NMCE_FLAT_UNROLL 2
-#endif
+// Launch shapes (the measured best of sweeps over block and unroll). The fold
+// order of the statistics kernel, and so its bits, depends on kStatsUnroll;
+// the flat backward's results do not depend on its shape.
 constexpr int kStatsBlock = 1024;
-constexpr int kStatsUnroll = NMCE_STATS_UNROLL;
+constexpr int kStatsUnroll = 2;
 constexpr int kBwdBlock = 1024;   // row-per-workgroup backward
 constexpr int kBwdUnroll = 4;
-constexpr int kFlatBlock = NMCE_FLAT_BLOCK;   // flat backward
-constexpr int kFlatUnroll = NMCE_FLAT_UNROLL;
+constexpr int kFlatBlock = 128;   // flat backward: 128 lanes x 2 vectors
+constexpr int kFlatUnroll = 2;
 constexpr int kValidateThreads = 256;
 // Running maxima start here instead of -inf so that rows (or lanes) that have
 // seen only -inf keep finite shifts and 2^(x-m) stays 0 rather than NaN.
