@@ -570,7 +570,27 @@ __global__ __launch_bounds__(kRedTokens * kRedSlices) void lmhead_reduce_partial
   const int64_t t = static_cast<int64_t>(blockIdx.x) * kRedTokens + tl;
   float m = kMaxFloorL, sum1 = -1.0f, tg = 0.0f;
   if (t < N) {
-    for (int64_t b = slice; b < nb; b += kRedSlices) {
+    // Eight blocks' loads in flight before they are merged, in block order
+    // as one at a time would (the same bits): a slice's walk was one L2 round
+    // trip per block.
+    constexpr int kAhead = 8;
+    int64_t b = slice;
+    for (; b + (kAhead - 1) * kRedSlices < nb; b += kAhead * kRedSlices) {
+      float xm[kAhead], xs[kAhead], xt[kAhead];
+#pragma unroll
+      for (int u = 0; u < kAhead; ++u) {
+        const int64_t o = (b + u * kRedSlices) * N + t;
+        xm[u] = pmax[o];
+        xs[u] = psum1[o];
+        xt[u] = ptgt[o];
+      }
+#pragma unroll
+      for (int u = 0; u < kAhead; ++u) {
+        merge_excess(m, sum1, xm[u], xs[u]);
+        tg += xt[u];
+      }
+    }
+    for (; b < nb; b += kRedSlices) {
       merge_excess(m, sum1, pmax[b * N + t], psum1[b * N + t]);
       tg += ptgt[b * N + t];
     }
