@@ -1817,6 +1817,8 @@ int check_fused_args(const void* hidden, const void* weight, int dtype, int64_t 
   // k-rows of P^T, W and X (MN-contiguous operands) must stay below 2 GiB;
   // ldt < 2^22 covers P^T, and operand_ok above bounds H.
   if (L.ldt >= (int64_t{1} << 22)) return NMCE_EINVAL_SHAPE;
+  // The dZ rescale's grid walks the 128-row blocks in its second dimension.
+  if (L.vpad / kRsRows > 65535) return NMCE_EINVAL_SHAPE;
   if (!workspace || workspace_bytes < L.total || !aligned16(workspace))
     return NMCE_EINVAL_WORKSPACE;
   return NMCE_OK;

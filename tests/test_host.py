@@ -118,6 +118,23 @@ def test_lmhead_argument_errors_before_launch(lib):
     assert lib.nmce_gemm_nt_bf16(p, 64, p, 64, 16, 16, 100, p, 0, 16, None) == -2
     assert lib.nmce_gemm_nt_bf16(p, 64, p, 64, 16, 16, 64, p, 7, 16, None) == -1
     assert lib.nmce_gemm_nt_bf16(p, 60, p, 64, 16, 16, 64, p, 0, 16, None) == -3
+    stats = lib.nmce_lmhead_ce_fused_chunk_stats
+    assert stats(p, p, 0, 16, 64, 100, p, 0, 0, 0, p, p, p, p, ws, None) == -1   # fp32
+    assert stats(p, p, 1, 16, 100, 100, p, 0, 0, 0, p, p, p, p, ws, None) == -2  # H % 64
+    assert stats(p, p, 1, 16, 64, 100, p, 0, 0, 1, p, p, p, p, ws, None) == -2   # chunk 1 of 1
+    assert stats(p, p, 1, 16, 64, 100, None, 0, 0, 0, p, p, p, p, ws, None) == -4
+    assert stats(p, p, 1, 16, 64, 100, p, 0, 0, 0, p, p, p, p, 16, None) == -6   # workspace
+    # The rescale's grid holds at most 65535 blocks of 128 vocabulary rows,
+    # and the vocabulary is padded to 256: 8388352 rows fit, one more does not.
+    assert stats(p, p, 1, 16, 64, 8388352, p, 0, 0, 0, p, p, p, p, 16, None) == -6
+    assert stats(p, p, 1, 16, 64, 8388353, p, 0, 0, 0, p, p, p, p, ws, None) == -2
+    grads = lib.nmce_lmhead_ce_fused_chunk_grads
+    assert grads(p, p, 1, 16, 64, 100, p, 0, 0, 0, p, p, p, p, 0, 0.0, p, p, p, ws,
+                 None) == -2  # gout_div must be positive
+    assert grads(p, p, 1, 16, 64, 100, p, 0, 0, 0, p, p, p, p, 0, 16.0, p, None, p, ws,
+                 None) == -4
+    assert grads(p, p, 1, 16, 64, 8388353, p, 0, 0, 0, p, p, p, p, 0, 16.0, p, p, p, ws,
+                 None) == -2
     mn = lib.nmce_gemm_mn_bf16
     assert mn(1, p, 16, p, 16, 16, 16, 100, p, 16, None) == -2  # k not a multiple of 64
     assert mn(1, p, 8, p, 16, 16, 16, 64, p, 16, None) == -3    # lda below m rounded to 8
