@@ -375,7 +375,8 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
  * token_chunk bf16). The one buffer that grows with both sizes is a chunk's
  * P, then dZ^T: bf16 [vocab_local, token_chunk], the size of the bf16 logits
  * when the chunk holds every token. The logits are computed once: 6 * n_rows * vocab_local *
- * hidden_size flops in all.
+ * hidden_size flops in all. vocab_local is at most 8388352 (65535 blocks of
+ * 128 rows once padded to 256); a larger shard is NMCE_EINVAL_SHAPE.
  * Replaces model.py:192 followed by cross_entropy.py:17-65 and the matmul
  * backward of model.py:192; with a caller that assumes the right upstream
  * value, as the reference's forward computes the softmax its backward
