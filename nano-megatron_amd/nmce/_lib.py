@@ -148,6 +148,3 @@ def stream_handle(device: torch.device) -> int:
         return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
 
-
-def ptr(t: torch.Tensor | None) -> int | None:
-    return None if t is None else t.data_ptr()
