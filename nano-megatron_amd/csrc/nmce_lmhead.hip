@@ -162,7 +162,7 @@ __device__ __forceinline__ void tile_coords(int group_m, int tiles_m, int tiles_
 // group of 16 lanes, lanes 4r .. 4r + 3 read 16 columns of k-row r and lane j
 // receives column j of the 4 rows), and the swizzle puts the 8 k-rows of one
 // read on distinct 16-byte bank groups, two rows per group.
-template <bool kAMN, bool kBMN>
+template <bool kAMN, bool kBMN, bool kStagger = true>
 __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, int64_t lda,
                                               int64_t M, const uint16_t* __restrict__ B,
                                               int64_t ldb, int64_t N, int64_t K, int64_t m0,
@@ -409,8 +409,25 @@ __device__ __forceinline__ void gemm_mainloop(const uint16_t* __restrict__ A, in
     // wave's loads and every wave's LDS reads of stage kt.
     wait_vmem();
     __syncthreads();
-    issue(static_cast<int>(kt & 1), k_at(kt + 2));
-    step(lds + static_cast<int>((kt + 1) & 1) * kStage, 0, f0, f1);
+    // With kStagger, the two waves of a SIMD (w and w + 4) issue their loads
+    // one sub-step apart: while one wave is issuing its eight
+    // buffer_load ... lds, the other still has MFMAs to issue, so the SIMD's
+    // MFMA pipe does not drain after every barrier (measured: every product
+    // of the one-pass fused step about 2% faster, the c4 step 1.5% and c5
+    // 1.8%; delaying waves 1, 3, 5, 7 or 2, 3, 6, 7 instead, so that both
+    // waves of a SIMD still issue together, is about 1% slower than no delay).
+    // The later half of the loads then has one sub-step less to arrive, which
+    // costs the recomputing path's products (operand rows 32-256 KiB apart)
+    // 1.5-9% and its dZ kernel 0.7%: they are built without it.
+    if constexpr (kStagger) {
+      const bool late = (wave & 4) != 0;
+      if (!late) issue(static_cast<int>(kt & 1), k_at(kt + 2));
+      step(lds + static_cast<int>((kt + 1) & 1) * kStage, 0, f0, f1);
+      if (late) issue(static_cast<int>(kt & 1), k_at(kt + 2));
+    } else {
+      issue(static_cast<int>(kt & 1), k_at(kt + 2));
+      step(lds + static_cast<int>((kt + 1) & 1) * kStage, 0, f0, f1);
+    }
   }
   {
     const char* st = lds + static_cast<int>((kt_n - 1) & 1) * kStage;
@@ -632,7 +649,7 @@ __global__ __launch_bounds__(kThreads) void lmhead_dz_kernel(
   tile_coords(kGroupM, tiles_m, tiles_n, tm, tn);
   const int64_t m0 = static_cast<int64_t>(tm) * kBM, n0 = static_cast<int64_t>(tn) * kBN;
   Acc acc;
-  gemm_mainloop<false, false>(Wc, H, Mvalid, X, H, N, H, m0, n0, lds, acc);
+  gemm_mainloop<false, false, /*kStagger=*/false>(Wc, H, Mvalid, X, H, N, H, m0, n0, lds, acc);
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -941,7 +958,8 @@ __device__ __forceinline__ void store_bf16_tile(const Acc& acc, char* lds,
 // accesses (the host checks them); otherwise the half tiles leave element by
 // element.
 // ---------------------------------------------------------------------------
-template <int kMode, bool kAMN = false, bool kBMN = false, bool kVec = true>
+template <int kMode, bool kAMN = false, bool kBMN = false, bool kVec = true,
+          bool kStagger = true>
 __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
     const uint16_t* __restrict__ A, int64_t lda, int64_t M, const uint16_t* __restrict__ B,
     int64_t ldb, int64_t N, int64_t K, uint16_t* __restrict__ C, float* __restrict__ Cf,
@@ -963,8 +981,8 @@ __global__ __launch_bounds__(kThreads) void gemm_store_kernel(
   const uint16_t* Bs = kBMN ? B + k0 * ldb : B + k0;
   Cf += split * split_stride;
   Acc acc;
-  gemm_mainloop<kAMN, kBMN>(As, lda, M, Bs, ldb, N, kl, m0, n0, lds, acc, ka_rows - k0,
-                            kb_rows - k0);
+  gemm_mainloop<kAMN, kBMN, kStagger>(As, lda, M, Bs, ldb, N, kl, m0, n0, lds, acc,
+                                      ka_rows - k0, kb_rows - k0);
   if constexpr (kMode != 0)
     store_f32_tile<kMode, kVec>(acc, lds, Cf, C, ldc, M, N, m0, n0);
   else
@@ -1326,7 +1344,7 @@ inline bool operand_ok(const void* p, int64_t ld) {
 // The product kernels by output mode and operand layout: K-contiguous A, and
 // B K-contiguous (b_mn = false) or MN-contiguous with kb_rows k-rows (b_mn;
 // then A may be MN-contiguous too, a_mn, in modes 0 and 1 only).
-template <int kMode, bool kAMN, bool kBMN, bool kVec>
+template <int kMode, bool kAMN, bool kBMN, bool kVec, bool kStagger = true>
 int launch_store(dim3 grid, hipStream_t stream, const uint16_t* A, int64_t lda, int64_t M,
                  const uint16_t* B, int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf,
                  int64_t ldc, int group_m, int64_t ka_rows, int64_t kb_rows, int splits,
@@ -1334,12 +1352,12 @@ int launch_store(dim3 grid, hipStream_t stream, const uint16_t* A, int64_t lda, 
   static bool lds_set = false;  // the attribute is set once per process and kernel
   if (!lds_set) {
     const hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&gemm_store_kernel<kMode, kAMN, kBMN, kVec>),
+        reinterpret_cast<const void*>(&gemm_store_kernel<kMode, kAMN, kBMN, kVec, kStagger>),
         hipFuncAttributeMaxDynamicSharedMemorySize, kLdsBytes);
     if (e != hipSuccess) return static_cast<int>(e);
     lds_set = true;
   }
-  hipLaunchKernelGGL((gemm_store_kernel<kMode, kAMN, kBMN, kVec>), grid, dim3(kThreads),
+  hipLaunchKernelGGL((gemm_store_kernel<kMode, kAMN, kBMN, kVec, kStagger>), grid, dim3(kThreads),
                      kLdsBytes, stream, A, lda, M, B, ldb, N, K, C, Cf, ldc, group_m, ka_rows,
                      kb_rows, splits, ks, split_stride);
   return NMCE_OK;
@@ -1351,7 +1369,8 @@ int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const
                       int64_t ldb, int64_t N, int64_t K, uint16_t* C, float* Cf, int64_t ldc,
                       hipStream_t stream, int group_m = kGroupM, bool a_mn = false,
                       bool b_mn = false, int64_t ka_rows = 0, int64_t kb_rows = 0,
-                      int splits = 1, int64_t ks = 0, int64_t split_stride = 0) {
+                      int splits = 1, int64_t ks = 0, int64_t split_stride = 0,
+                      bool stagger = true) {
   if (splits < 1 || (splits > 1 && (mode != 1 || ks <= 0 || ks % kBK != 0 ||
                                     (splits - 1) * ks >= K)))
     return NMCE_EINVAL_SHAPE;
@@ -1373,6 +1392,15 @@ int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const
            : launch_store<MODE, AMN, BMN, false>(grid, stream, A, lda, M, B, ldb, N, K, C, Cf, \
                                                  ldc, group_m, ka_rows, kb_rows, splits, ks,  \
                                                  split_stride)
+  // Both operands K-contiguous, loads issued together (stagger = false).
+#define NMCE_STORE_FLAT(MODE)                                                                   \
+  st = vec ? launch_store<MODE, false, false, true, false>(grid, stream, A, lda, M, B, ldb, N, K, \
+                                                           C, Cf, ldc, group_m, ka_rows, kb_rows, \
+                                                           splits, ks, split_stride)              \
+           : launch_store<MODE, false, false, false, false>(grid, stream, A, lda, M, B, ldb, N,   \
+                                                            K, C, Cf, ldc, group_m, ka_rows,      \
+                                                            kb_rows, splits, ks, split_stride)
+  if (!stagger && (a_mn || b_mn)) return NMCE_EINVAL_SHAPE;  // built for K-contiguous only
   if (a_mn) {
     if (mode == 0) NMCE_STORE(0, true, true);
     else NMCE_STORE(1, true, true);
@@ -1383,14 +1411,22 @@ int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const
       case 2: NMCE_STORE(2, false, true); break;
       default: NMCE_STORE(3, false, true); break;
     }
-  } else {
+  } else if (stagger) {
     switch (mode) {
       case 0: NMCE_STORE(0, false, false); break;
       case 1: NMCE_STORE(1, false, false); break;
       case 2: NMCE_STORE(2, false, false); break;
       default: NMCE_STORE(3, false, false); break;
     }
+  } else {
+    switch (mode) {
+      case 0: NMCE_STORE_FLAT(0); break;
+      case 1: NMCE_STORE_FLAT(1); break;
+      case 2: NMCE_STORE_FLAT(2); break;
+      default: NMCE_STORE_FLAT(3); break;
+    }
   }
+#undef NMCE_STORE_FLAT
 #undef NMCE_STORE
   if (st) return st;
   return launch_status();
@@ -1779,7 +1815,7 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
       return st;
     // dW rows [v0, v0 + mvalid) = dZ^T_c X  (K = tokens, padded with zeros).
     if ((st = launch_gemm_store(0, dzt, L.ldt, mvalid, xt, L.ldt, H, L.ldt, dW + v0 * H, nullptr,
-                                H, s)))
+                                H, s, kGroupM, false, false, 0, 0, 1, 0, 0, /*stagger=*/false)))
       return st;
     // dX (+)= dZ_c W_c  (K = the chunk's padded vocabulary rows).
     int mode;
@@ -1788,7 +1824,7 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
     else if (c + 1 < L.n_chunks) mode = 2;
     else mode = 3;
     if ((st = launch_gemm_store(mode, dz, L.chunk, n_rows, wt + v0, L.vpad, H, mpad, dX, acc, H,
-                                s)))
+                                s, kGroupM, false, false, 0, 0, 1, 0, 0, /*stagger=*/false)))
       return st;
   }
   return NMCE_OK;
