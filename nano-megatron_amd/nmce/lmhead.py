@@ -69,10 +69,10 @@ DEFAULT_VOCAB_CHUNK = 32768
 # default at most a quarter of the tokens (rounded up to whole 256-token
 # tiles; every token only when there are at most 256) and at most
 # CHUNK_BUDGET_BYTES, so nothing the size of the [tokens, V] logits is
-# allocated. dW is then accumulated in fp32 across the chunks, which the
-# accumulating GEMM epilogue does at little cost (measured on one MI355X:
-# [16384, 4096] x [128256, 4096] runs as fast in four chunks of 4096 tokens as
-# in one chunk; [16384, 3072] x [256000, 3072] 3% slower).
+# allocated. dW is then accumulated in fp32 across the chunks by the GEMM
+# epilogue (measured on one MI355X: [16384, 4096] x [128256, 4096] 3.4% slower
+# in four chunks of 4096 tokens than in one chunk, [16384, 3072] x
+# [256000, 3072] 1.6%).
 CHUNK_BUDGET_BYTES = 2 << 30
 CHUNK_FRACTION = 4
 
