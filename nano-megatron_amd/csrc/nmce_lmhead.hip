@@ -1432,6 +1432,17 @@ int launch_gemm_store(int mode, const uint16_t* A, int64_t lda, int64_t M, const
   return launch_status();
 }
 
+// A product with both operands K-contiguous whose stage loads are issued by
+// all waves together (gemm_mainloop's kStagger off): the recomputing path's
+// products, whose operand rows lie far apart.
+int launch_gemm_store_unstaggered(int mode, const uint16_t* A, int64_t lda, int64_t M,
+                                  const uint16_t* B, int64_t ldb, int64_t N, int64_t K,
+                                  uint16_t* C, float* Cf, int64_t ldc, hipStream_t stream) {
+  return launch_gemm_store(mode, A, lda, M, B, ldb, N, K, C, Cf, ldc, stream, kGroupM,
+                           /*a_mn=*/false, /*b_mn=*/false, 0, 0, /*splits=*/1, 0, 0,
+                           /*stagger=*/false);
+}
+
 int launch_transpose(const uint16_t* in, int64_t R, int64_t C, int64_t ldi, uint16_t* out,
                      int64_t ldo, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>((C + 63) / 64), static_cast<unsigned>((ldo + 63) / 64));
@@ -1814,8 +1825,8 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
                      grad_output, gout_stride, c, L, ws, s)))
       return st;
     // dW rows [v0, v0 + mvalid) = dZ^T_c X  (K = tokens, padded with zeros).
-    if ((st = launch_gemm_store(0, dzt, L.ldt, mvalid, xt, L.ldt, H, L.ldt, dW + v0 * H, nullptr,
-                                H, s, kGroupM, false, false, 0, 0, 1, 0, 0, /*stagger=*/false)))
+    if ((st = launch_gemm_store_unstaggered(0, dzt, L.ldt, mvalid, xt, L.ldt, H, L.ldt,
+                                            dW + v0 * H, nullptr, H, s)))
       return st;
     // dX (+)= dZ_c W_c  (K = the chunk's padded vocabulary rows).
     int mode;
@@ -1823,8 +1834,8 @@ int nmce_lmhead_ce_bwd(const void* hidden, const void* weight, int dtype, int64_
     else if (c == 0) mode = 1;
     else if (c + 1 < L.n_chunks) mode = 2;
     else mode = 3;
-    if ((st = launch_gemm_store(mode, dz, L.chunk, n_rows, wt + v0, L.vpad, H, mpad, dX, acc, H,
-                                s, kGroupM, false, false, 0, 0, 1, 0, 0, /*stagger=*/false)))
+    if ((st = launch_gemm_store_unstaggered(mode, dz, L.chunk, n_rows, wt + v0, L.vpad, H, mpad,
+                                            dX, acc, H, s)))
       return st;
   }
   return NMCE_OK;
